@@ -1,0 +1,177 @@
+"""Benchmark: ms per 10-step Pi0 action chunk (hipGraph replay of the decoder loop).
+
+One "step" of this benchmark = one replay of the captured decoder loop: 10
+Euler steps x 18 layers at M = 51 rows against 819 keys,
+with weights, prefix K/V and inputs already resident in HBM.
+
+Also measured, inside the same run:
+  * the dominant kernel (the GeGLU gate/up GEMM, 47% of the bytes) timed with
+    HIP events around a captured graph of launches cycling the 18 distinct
+    layer weights (cold reads), -> `roofline`;
+  * the CPU oracle (fp32 PyTorch restatement) on a bounded
+    sample of whole chunks on the host cores, -> `cpu_baseline`.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "flash-vla_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+LAYERS, STEPS, ENC_LEN, CHUNK = 18, 10, 768, 50
+LAYER_WEIGHT_BYTES = 34_603_008            # qkv + o + gate + up + down, bf16
+SMALL_PROJ_BYTES = 2_232_384               # in/mlp/out projections and biases per step
+KV_READ_BYTES = LAYERS * 819 * 256 * 2 * 2
+KV_WRITE_BYTES = LAYERS * 51 * 256 * 2 * 2
+STEP_BYTES = LAYERS * LAYER_WEIGHT_BYTES + SMALL_PROJ_BYTES + KV_READ_BYTES + KV_WRITE_BYTES
+CHUNK_BYTES = STEPS * STEP_BYTES           # 6,411,223,680 B
+GATE_BYTES = 2 * 1024 * 4096 * 2           # gate + up weights of one layer (activations excluded)
+
+
+def _time_graph(run, n_inner, reps, torch):
+    """Median microseconds per call of `run(i)` captured n_inner times in one graph."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(3):
+            run(i)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n_inner):
+            run(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    samples = []
+    for _ in range(reps):
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        g.replay()
+        e.record(stream)
+        e.synchronize()
+        samples.append(s.elapsed_time(e) * 1000.0 / n_inner)
+    return statistics.median(samples)
+
+
+def kernel_roofline(eng, torch):
+    from flash_vla_amd.backends.hip import wrappers as W
+    b, w = eng.buffers, eng.weights
+    with W.use_pool(eng.pool):
+        us = _time_graph(lambda i: W.decoder_norm_gated_ffn(
+            b["decoder_x"], w["decoder_ffn_gate_w"][i % LAYERS], w["decoder_ffn_up_w"][i % LAYERS],
+            b["decoder_hidden"], None), n_inner=LAYERS * 4, reps=20, torch=torch)
+    achieved = GATE_BYTES / (us * 1e-6) / 1e9
+    return {"kernel": "skinny_gemm_kernel<EPI_GATE> (decoder_norm_gated_ffn)",
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "avg_launch_us": round(us, 3), "bytes_per_launch": GATE_BYTES}
+
+
+def cpu_baseline(seconds_budget: float = 20.0):
+    import torch
+    from oracle import pi0_decoder as O
+    from flash_vla_amd.weights import decoder_checkpoint, decoder_inputs
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    ck = decoder_checkpoint(seed=0)
+    inp = decoder_inputs(seed=1)
+    args = (ck, inp["observation_state_normalized"], inp["diffusion_noise"], inp["encoder_K"],
+            inp["encoder_V"], ENC_LEN)
+    O.decoder_packed(*args, steps=1, bf16=False)       # warm caches / thread pool
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < seconds_budget and len(times) < 10):
+        t0 = time.perf_counter()
+        O.decoder_packed(*args, steps=STEPS, bf16=False)
+        times.append((time.perf_counter() - t0) * 1000.0)
+        if time.perf_counter() - t_start > 3 * seconds_budget:
+            break
+    return {"value": round(statistics.median(times), 2), "unit": "ms per 10-step chunk",
+            "cores": threads, "kind": "port",
+            "sample": f"median of {len(times)} full 10-step chunks (fp32 PyTorch oracle, "
+                      f"config 1 maths on the packed bf16 weights)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-kernel", action="store_true", help="skip the per-kernel roofline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the decoder loop is a single-GPU path); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from flash_vla_amd import Pi0DecoderEngine
+    from flash_vla_amd.weights import decoder_checkpoint, decoder_inputs
+
+    t0 = time.time()
+    ck = decoder_checkpoint(seed=0)
+    inp = decoder_inputs(seed=1)
+    print(f"[bench] inputs generated in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    eng = Pi0DecoderEngine({k: v.cuda() for k, v in ck.items()}, steps=STEPS, layers=LAYERS)
+    eng.load_prefix(inp["encoder_K"].cuda(), inp["encoder_V"].cuda())
+    state = inp["observation_state_normalized"].cuda()
+    noise = inp["diffusion_noise"].cuda()
+    eng.buffers["observation_state_normalized"].copy_(state)
+    print(f"[bench] engine captured, {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        eng.buffers["diffusion_noise"].copy_(noise)
+        eng.replay()
+    torch.cuda.synchronize()
+    # timed region: exactly `steps` chunk replays (the noise is not reset in between;
+    # each replay is a full 10-step denoise of whatever the buffer holds)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(args.steps):
+        eng.replay()
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    print(f"[bench] {ms:.3f} ms/chunk", file=sys.stderr, flush=True)
+
+    roof = None if args.no_kernel else kernel_roofline(eng, torch)
+    cpu = None if args.no_cpu else cpu_baseline()
+
+    gbs = CHUNK_BYTES / (ms * 1e-3) / 1e9
+    out = {
+        "metric": "ms per 10-step action chunk (decoder loop, hipGraph)",
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) folded weights, N(0,1) prefix K/V, state, noise)",
+        "config": {"workload": "Pi0 decoder loop, BASELINE config 2: 10 Euler steps x 18 layers, "
+                               "M=51 rows (1 state + 50 actions), 8 q heads / 1 kv head x 256, "
+                               "keys 819, width 1024, FFN 4096, batch 1",
+                   "global_batch": 1, "seq_len": 51, "keys": 819, "parallelism": "single GPU"},
+        "ms_per_decoder_step": round(ms / STEPS, 4),
+        "hbm_gbs": round(gbs, 1),
+        "loop_roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "bytes_per_chunk": CHUNK_BYTES,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

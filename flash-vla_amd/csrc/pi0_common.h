@@ -1,0 +1,61 @@
+// Shared device helpers for the gfx950 Pi0 decoder kernels.
+//
+// Conventions used by every kernel in this library:
+//  * activations are bf16, row-major, with an explicit leading dimension;
+//  * weights are consumed in a "B-fragment" packed layout produced once by
+//    pi0hip_pack_weight (see pi0_gemm.hip): for W[K][N] the tile (kt, nt) of
+//    32 k x 16 n is 64 lanes x 8 bf16, lane = (k%32/8)*16 + n%16, element k%8,
+//    tiles ordered [nt][kt] so that one column tile is a contiguous stream;
+//  * the MFMA is v_mfma_f32_16x16x32_bf16: A lane l holds A[l%16][8*(l/16)+j],
+//    B lane l holds B[8*(l/16)+j][l%16], C lane l holds C[4*(l/16)+i][l%16].
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define PI0_WAVE 64
+
+namespace pi0 {
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float bf2f(__bf16 v) { return static_cast<float>(v); }
+__device__ __forceinline__ __bf16 f2bf(float v) { return static_cast<__bf16>(v); }
+// Round an fp32 value to the nearest bf16 and return it as fp32.
+__device__ __forceinline__ float round_bf(float v) { return bf2f(f2bf(v)); }
+
+__device__ __forceinline__ bf16x8 load8(const __bf16* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+__device__ __forceinline__ bf16x8 zero8() {
+  u32x4 z = {0u, 0u, 0u, 0u};
+  return __builtin_bit_cast(bf16x8, z);
+}
+__device__ __forceinline__ f32x4 zero4() {
+  f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  return z;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Gemma tanh-GELU written as v * sigmoid(2*sqrt(2/pi) * (v + 0.044715 v^3)).
+__device__ __forceinline__ float gelu_tanh(float v) {
+  const float c0 = 1.5957691216057308f, c1 = 0.044715f;
+  return v / (1.0f + __expf(-(c0 * v * (1.0f + c1 * v * v))));
+}
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+
+__device__ __forceinline__ float warp_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, PI0_WAVE);
+  return v;
+}
+
+}  // namespace pi0

@@ -1,0 +1,371 @@
+// Skinny bf16 MFMA GEMMs for the Pi0 decoder (M <= 64 rows per block).
+//
+// Every decoder projection is C[M, N] = x[M, K] @ W[K, N] with M = 50 or 51:
+// the cost is streaming W from HBM once. One workgroup (4 waves) owns a
+// 16-column tile of W and a K range; each wave issues all of its weight loads
+// (16 bytes per lane, one contiguous 1 KB packed fragment per instruction)
+// before the first MFMA so that the whole slice is in flight at once. The
+// activation rows come from L2 as MFMA A fragments. Waves split K; their
+// accumulators are summed in LDS. When the column tiles alone cannot fill the
+// chip (N = 1024), K is also split across workgroups and the last workgroup
+// to finish a tile (an atomic arrival counter, reset by that workgroup) sums
+// the fp32 partials in split order -- deterministic -- and runs the epilogue.
+//
+// The epilogues are the decoder's fused call sites (reference file:line):
+//   EPI_BIAS        x@W + b                    decoder_action_mlp  (wrappers.py:123-128)
+//   EPI_RES         out += x@W                 o-proj / ffn-down   (wrappers.py:176-189)
+//   EPI_RMS_BIAS_RES out += b + f * x@W        action out-proj     (fused_norm.py:81-125)
+//   EPI_QKV_ROPE    f * x@W, RoPE, scatter     qkv + rope          (base.py:607-669)
+//   EPI_GATE        gelu(f x@Wg) * (f x@Wu)    gated FFN           (fused_norm.py:26-78)
+// with f = bf16(rsqrt(mean_k x^2 + 1e-6)) computed from the same A fragments.
+#include "pi0_common.h"
+#include "pi0_hip.h"
+
+namespace pi0 {
+
+enum Epi { EPI_BIAS = 0, EPI_RES = 1, EPI_RMS_BIAS_RES = 2, EPI_QKV_ROPE = 3, EPI_GATE = 4 };
+
+struct GemmArgs {
+  const __bf16* x; int ldx;
+  const __bf16* w0; const __bf16* w1;
+  const __bf16* bias;
+  __bf16* out; int ldo;
+  __bf16* out_k; __bf16* out_v; int ldkv;
+  const __bf16* rope;
+  __bf16* norm_factor;
+  float* ws; int* counters;
+  int M, N, K, splitk, heads, head_dim;
+};
+
+constexpr bool uses_rms(int epi) {
+  return epi == EPI_RMS_BIAS_RES || epi == EPI_QKV_ROPE || epi == EPI_GATE;
+}
+
+// Per-tile scratch layout inside the workspace: [mb][nt][ks][64 rows][16 * ND] fp32,
+// then [mb][nt][ks][64] fp32 sums of squares. Counters live in a separate int array.
+__host__ __device__ inline size_t part_floats(int tiles, int splitk, int nd) {
+  return (size_t)tiles * splitk * 64 * 16 * nd;
+}
+
+template <int EPI, bool DUAL, int KTW>
+__global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
+  constexpr int ND = DUAL ? 2 : 1;
+  constexpr bool RMS = uses_rms(EPI);
+  __shared__ float red[ND][4][4][4][PI0_WAVE];   // [acc][wave][mt][i][lane]
+  __shared__ float ssred[4][4][PI0_WAVE];        // [wave][mt][lane]
+  __shared__ int s_last;
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int splitk = a.splitk;
+  const int nt = blockIdx.x / splitk, ks = blockIdx.x - nt * splitk;
+  const int ntiles = a.N >> 4;
+  const int mb = blockIdx.y, m0 = mb * 64;
+  const int KT = a.K >> 5;
+  const int kt0 = ks * (KT / splitk) + wave * KTW;
+
+  // ---- weight stream: all fragments of this wave in flight together
+  bf16x8 b0[KTW], b1[KTW];
+  {
+    const __bf16* wp = a.w0 + ((size_t)nt * KT + kt0) * 512 + lane * 8;
+#pragma unroll
+    for (int i = 0; i < KTW; ++i) b0[i] = load8(wp + i * 512);
+    if constexpr (DUAL) {
+      const __bf16* wq = a.w1 + ((size_t)nt * KT + kt0) * 512 + lane * 8;
+#pragma unroll
+      for (int i = 0; i < KTW; ++i) b1[i] = load8(wq + i * 512);
+    }
+  }
+  // ---- activation fragments (rows past M read as zero)
+  const int r = lane & 15, g = lane >> 4;
+  bf16x8 av[4][KTW];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int row = m0 + mt * 16 + r;
+    const __bf16* xp = a.x + (size_t)row * a.ldx + kt0 * 32 + g * 8;
+#pragma unroll
+    for (int i = 0; i < KTW; ++i) av[mt][i] = row < a.M ? load8(xp + i * 32) : zero8();
+  }
+
+  f32x4 acc0[4], acc1[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) { acc0[mt] = zero4(); acc1[mt] = zero4(); }
+#pragma unroll
+  for (int i = 0; i < KTW; ++i) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      acc0[mt] = mfma16(av[mt][i], b0[i], acc0[mt]);
+      if constexpr (DUAL) acc1[mt] = mfma16(av[mt][i], b1[i], acc1[mt]);
+    }
+  }
+
+  // ---- intra-workgroup reduction over the 4 waves' K ranges
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      red[0][wave][mt][i][lane] = acc0[mt][i];
+      if constexpr (DUAL) red[ND - 1][wave][mt][i][lane] = acc1[mt][i];
+    }
+  }
+  if constexpr (RMS) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < KTW; ++i) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) { float v = bf2f(av[mt][i][j]); s += v * v; }
+      }
+      ssred[wave][mt][lane] = s;
+    }
+  }
+  __syncthreads();
+
+  // thread t owns row t/4 (of 64) and columns 4*(t%4) .. +3 of the tile
+  const int lrow = t >> 2, c4 = (t & 3) * 4;
+  const int mt = lrow >> 4, r16 = lrow & 15, ii = r16 & 3, gg = r16 >> 2;
+  float v0[4], v1[4], ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      s0 += red[0][w][mt][ii][gg * 16 + c4 + c];
+      if constexpr (DUAL) s1 += red[ND - 1][w][mt][ii][gg * 16 + c4 + c];
+    }
+    v0[c] = s0; v1[c] = s1;
+  }
+  if constexpr (RMS) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ss += ssred[w][mt][q * 16 + r16];
+  }
+
+  // ---- split-K across workgroups: last arrival sums partials in split order
+  if (splitk > 1) {
+    const int tile = mb * ntiles + nt;
+    const size_t tiles = (size_t)gridDim.y * ntiles;
+    float* part = a.ws;
+    float* ssp = a.ws + part_floats((int)tiles, splitk, ND);
+    {
+      float* p = part + (((size_t)tile * splitk + ks) * 64 + lrow) * 16 * ND + c4;
+      *reinterpret_cast<f32x4*>(p) = f32x4{v0[0], v0[1], v0[2], v0[3]};
+      if constexpr (DUAL) *reinterpret_cast<f32x4*>(p + 16) = f32x4{v1[0], v1[1], v1[2], v1[3]};
+      if (RMS && (t & 3) == 0) ssp[((size_t)tile * splitk + ks) * 64 + lrow] = ss;
+    }
+    __threadfence();
+    __syncthreads();
+    if (t == 0) {
+      const int prev = atomicAdd(&a.counters[tile], 1);
+      const int last = prev == splitk - 1;
+      if (last) atomicExch(&a.counters[tile], 0);
+      __threadfence();
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) { v0[c] = 0.f; v1[c] = 0.f; }
+    ss = 0.f;
+    for (int k = 0; k < splitk; ++k) {
+      const float* p = part + (((size_t)tile * splitk + k) * 64 + lrow) * 16 * ND + c4;
+      const f32x4 q0 = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v0[c] += q0[c];
+      if constexpr (DUAL) {
+        const f32x4 q1 = *reinterpret_cast<const f32x4*>(p + 16);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v1[c] += q1[c];
+      }
+      if constexpr (RMS) ss += ssp[((size_t)tile * splitk + k) * 64 + lrow];
+    }
+  }
+
+  // ---- epilogue
+  const int row = m0 + lrow;
+  if (row >= a.M) return;
+  const int n = nt * 16 + c4;
+  float f = 1.f;
+  if constexpr (RMS) f = round_bf(rsqrtf(ss / (float)a.K + 1e-6f));
+
+  float o[4];
+  if constexpr (EPI == EPI_BIAS) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = v0[c] + bf2f(a.bias[n + c]);
+  } else if constexpr (EPI == EPI_RES) {
+    const __bf16* rp = a.out + (size_t)row * a.ldo + n;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = v0[c] + bf2f(rp[c]);
+  } else if constexpr (EPI == EPI_RMS_BIAS_RES) {
+    const __bf16* rp = a.out + (size_t)row * a.ldo + n;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = v0[c] * f + bf2f(a.bias[n + c]) + bf2f(rp[c]);
+  } else if constexpr (EPI == EPI_GATE) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = gelu_tanh(v0[c] * f) * (v1[c] * f);
+  } else if constexpr (EPI == EPI_QKV_ROPE) {
+    const int hd = a.head_dim, qdim = a.heads * hd;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = v0[c] * f;
+    if (n < qdim + hd) {
+      const int rj = n % hd;
+      const __bf16* rp = a.rope + (size_t)row * hd + rj;
+#pragma unroll
+      for (int p = 0; p < 4; p += 2) {
+        const float cs = bf2f(rp[p]), sn = bf2f(rp[p + 1]);
+        const float x0 = o[p], x1 = o[p + 1];
+        o[p] = x0 * cs - x1 * sn;
+        o[p + 1] = x1 * cs + x0 * sn;
+      }
+    }
+    __bf16* dst;
+    if (n < qdim) dst = a.out + (size_t)row * qdim + n;
+    else if (n < qdim + hd) dst = a.out_k + (size_t)row * a.ldkv + (n - qdim);
+    else dst = a.out_v + (size_t)row * a.ldkv + (n - qdim - hd);
+    bf16x4 pk = {f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
+    *reinterpret_cast<bf16x4*>(dst) = pk;
+    if (a.norm_factor && nt == 0 && (t & 3) == 0) a.norm_factor[row] = f2bf(f);
+    return;
+  }
+  bf16x4 pk = {f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
+  *reinterpret_cast<bf16x4*>(a.out + (size_t)row * a.ldo + n) = pk;
+}
+
+template <int EPI, bool DUAL>
+static int launch_gemm(const GemmArgs& a, hipStream_t s) {
+  if (a.M <= 0 || a.N <= 0 || a.K <= 0) return PI0HIP_ERR_ARG;
+  if (a.K % 32 || a.N % 16 || a.splitk < 1) return PI0HIP_ERR_SHAPE;
+  const int KT = a.K / 32;
+  if (KT % (4 * a.splitk)) return PI0HIP_ERR_SHAPE;
+  if (a.splitk > 1 && (!a.ws || !a.counters)) return PI0HIP_ERR_WORKSPACE;
+  const int ktw = KT / (4 * a.splitk);
+  dim3 grid((a.N / 16) * a.splitk, (a.M + 63) / 64);
+  switch (ktw) {
+    case 1: skinny_gemm_kernel<EPI, DUAL, 1><<<grid, 256, 0, s>>>(a); break;
+    case 2: skinny_gemm_kernel<EPI, DUAL, 2><<<grid, 256, 0, s>>>(a); break;
+    case 4: skinny_gemm_kernel<EPI, DUAL, 4><<<grid, 256, 0, s>>>(a); break;
+    case 8: skinny_gemm_kernel<EPI, DUAL, 8><<<grid, 256, 0, s>>>(a); break;
+    default: return PI0HIP_ERR_SHAPE;
+  }
+  return (int)hipGetLastError();
+}
+
+// W[batch][K][N] row-major -> packed B fragments, one thread per 16-byte fragment row.
+__global__ void pack_weight_kernel(const __bf16* __restrict__ w, __bf16* __restrict__ p,
+                                   int K, int N, long long total_frags) {
+  const long long f = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (f >= total_frags) return;
+  const long long per = (long long)(K / 32) * (N / 16) * 64;
+  const long long b = f / per;
+  long long rem = f - b * per;
+  const int lane = (int)(rem & 63);
+  rem >>= 6;
+  const int KT = K / 32;
+  const int kt = (int)(rem % KT), nt = (int)(rem / KT);
+  const int n = nt * 16 + (lane & 15);
+  const int k0 = kt * 32 + (lane >> 4) * 8;
+  const __bf16* src = w + b * (long long)K * N + (long long)k0 * N + n;
+  bf16x8 v;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = src[(long long)j * N];
+  *reinterpret_cast<bf16x8*>(p + f * 8) = v;
+}
+
+}  // namespace pi0
+
+using namespace pi0;
+
+static inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+extern "C" {
+
+size_t pi0hip_gemm_workspace_bytes(int M, int N, int splitk, int dual) {
+  if (splitk <= 1) return 0;
+  const size_t tiles = (size_t)((M + 63) / 64) * (N / 16);
+  const int nd = dual ? 2 : 1;
+  const size_t floats = part_floats((int)tiles, splitk, nd) + tiles * splitk * 64;
+  return round_up(tiles * sizeof(int), 256) + floats * sizeof(float);
+}
+
+static int setup_ws(GemmArgs& a, void* ws, size_t ws_bytes, int dual) {
+  if (a.splitk <= 1) { a.ws = nullptr; a.counters = nullptr; return 0; }
+  const size_t need = pi0hip_gemm_workspace_bytes(a.M, a.N, a.splitk, dual);
+  if (!ws || ws_bytes < need) return PI0HIP_ERR_WORKSPACE;
+  const size_t tiles = (size_t)((a.M + 63) / 64) * (a.N / 16);
+  a.counters = reinterpret_cast<int*>(ws);
+  a.ws = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + round_up(tiles * sizeof(int), 256));
+  return 0;
+}
+
+static GemmArgs base_args(const void* x, int ldx, const void* w, void* out, int ldo,
+                          int M, int N, int K, int splitk) {
+  GemmArgs a = {};
+  a.x = (const __bf16*)x; a.ldx = ldx; a.w0 = (const __bf16*)w;
+  a.out = (__bf16*)out; a.ldo = ldo;
+  a.M = M; a.N = N; a.K = K; a.splitk = splitk;
+  return a;
+}
+
+int pi0hip_pack_weight(const void* w, void* packed, int K, int N, int batch, hipStream_t s) {
+  if (!w || !packed || K <= 0 || N <= 0 || batch <= 0) return PI0HIP_ERR_ARG;
+  if (K % 32 || N % 16) return PI0HIP_ERR_SHAPE;
+  const long long frags = (long long)batch * (K / 32) * (N / 16) * 64;
+  const int threads = 256;
+  const long long blocks = (frags + threads - 1) / threads;
+  hipLaunchKernelGGL(pack_weight_kernel, dim3((unsigned)blocks), dim3(threads), 0, s,
+                     (const __bf16*)w, (__bf16*)packed, K, N, frags);
+  return (int)hipGetLastError();
+}
+
+int pi0hip_linear_bias(const void* x, int ldx, const void* wp, const void* bias, void* out,
+                       int ldo, int M, int N, int K, int splitk, void* ws, size_t ws_bytes,
+                       hipStream_t s) {
+  if (!x || !wp || !bias || !out) return PI0HIP_ERR_ARG;
+  GemmArgs a = base_args(x, ldx, wp, out, ldo, M, N, K, splitk);
+  a.bias = (const __bf16*)bias;
+  if (int e = setup_ws(a, ws, ws_bytes, 0)) return e;
+  return launch_gemm<EPI_BIAS, false>(a, s);
+}
+
+int pi0hip_linear_residual(const void* x, int ldx, const void* wp, void* out, int ldo,
+                           int M, int N, int K, int splitk, void* ws, size_t ws_bytes,
+                           hipStream_t s) {
+  if (!x || !wp || !out) return PI0HIP_ERR_ARG;
+  GemmArgs a = base_args(x, ldx, wp, out, ldo, M, N, K, splitk);
+  if (int e = setup_ws(a, ws, ws_bytes, 0)) return e;
+  return launch_gemm<EPI_RES, false>(a, s);
+}
+
+int pi0hip_rms_linear_bias_residual(const void* x, int ldx, const void* wp, const void* bias,
+                                    void* out, int ldo, int M, int N, int K, int splitk,
+                                    void* ws, size_t ws_bytes, hipStream_t s) {
+  if (!x || !wp || !bias || !out) return PI0HIP_ERR_ARG;
+  GemmArgs a = base_args(x, ldx, wp, out, ldo, M, N, K, splitk);
+  a.bias = (const __bf16*)bias;
+  if (int e = setup_ws(a, ws, ws_bytes, 0)) return e;
+  return launch_gemm<EPI_RMS_BIAS_RES, false>(a, s);
+}
+
+int pi0hip_norm_qkv_rope(const void* x, int ldx, const void* wp, const void* rope, void* q,
+                         void* k, void* v, int ldkv, void* norm_factor, int M, int K,
+                         int heads, int head_dim, hipStream_t s) {
+  if (!x || !wp || !rope || !q || !k || !v) return PI0HIP_ERR_ARG;
+  if (head_dim % 16 || heads <= 0) return PI0HIP_ERR_SHAPE;
+  GemmArgs a = base_args(x, ldx, wp, q, heads * head_dim, M, (heads + 2) * head_dim, K, 1);
+  a.out_k = (__bf16*)k; a.out_v = (__bf16*)v; a.ldkv = ldkv;
+  a.rope = (const __bf16*)rope; a.norm_factor = (__bf16*)norm_factor;
+  a.heads = heads; a.head_dim = head_dim;
+  return launch_gemm<EPI_QKV_ROPE, false>(a, s);
+}
+
+int pi0hip_norm_gated_ffn(const void* x, int ldx, const void* gate_p, const void* up_p,
+                          void* out, int ldo, int M, int N, int K, hipStream_t s) {
+  if (!x || !gate_p || !up_p || !out) return PI0HIP_ERR_ARG;
+  GemmArgs a = base_args(x, ldx, gate_p, out, ldo, M, N, K, 1);
+  a.w1 = (const __bf16*)up_p;
+  return launch_gemm<EPI_GATE, true>(a, s);
+}
+
+}  // extern "C"

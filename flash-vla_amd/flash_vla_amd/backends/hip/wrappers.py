@@ -1,0 +1,303 @@
+"""HIP backend call-site wrappers for the Pi0 decoder.
+
+One function per op-table entry, with the reference's signatures
+(`backends/tilelang/wrappers.py:108-221`, `fused_wrappers.py:45-122`): tensors
+in, destinations written in place, return value = the destination. Each
+wrapper checks dtype / layout / shape on the host, maps tensors to raw
+pointers and calls one C-ABI entry point of libpi0hip.so on the current
+stream. Nothing here allocates after warmup: workspaces come from the active
+ScratchPool and packed weights from the packed-weight cache, both filled
+during warmup and frozen before capture.
+"""
+from __future__ import annotations
+
+import contextlib
+
+import torch
+
+from ...arena import ScratchPool
+from . import _abi
+
+DECODER_HEADS = 8
+_POOL = ScratchPool()
+
+
+def set_pool(pool: ScratchPool) -> None:
+    global _POOL
+    _POOL = pool
+
+
+@contextlib.contextmanager
+def use_pool(pool: ScratchPool):
+    """Route scratch allocation through `pool` (as `wrappers.py:42-51` of the reference)."""
+    global _POOL
+    previous = _POOL
+    _POOL = pool
+    try:
+        yield
+    finally:
+        _POOL = previous
+
+
+def scratch(role: str, shape, dtype, device) -> torch.Tensor:
+    return _POOL.get(role, shape, dtype, device)
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _capturing() -> bool:
+    return torch.cuda.is_current_stream_capturing()
+
+
+def _check(t: torch.Tensor, name: str, ndim: int | None = None) -> None:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name}: expected bfloat16, got {t.dtype}")
+    if not t.is_cuda:
+        raise ValueError(f"{name}: expected a GPU tensor")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name}: expected {ndim} dims, got shape {tuple(t.shape)}")
+    if t.dim() >= 1 and t.stride(-1) != 1:
+        raise ValueError(f"{name}: last dimension must be contiguous")
+
+
+def _ptr(t: torch.Tensor):
+    return t.data_ptr()
+
+
+# ---------------------------------------------------------------------------
+# Packed weights: the kernels stream W[K, N] in MFMA B-fragment order. A weight
+# is packed once (a whole [L, K, N] stack at a time when it is a layer view)
+# and looked up by address on every later call.
+# ---------------------------------------------------------------------------
+class _PackedEntry:
+    __slots__ = ("src", "packed", "base", "nbytes", "K", "N", "version")
+
+    def __init__(self, src, packed, K, N):
+        self.src, self.packed, self.K, self.N = src, packed, K, N
+        self.base = src.data_ptr()
+        self.nbytes = src.numel() * src.element_size()
+        self.version = src._version
+
+
+_PACKED: list[_PackedEntry] = []
+
+
+def _pack_into(src: torch.Tensor, dst: torch.Tensor, K: int, N: int) -> None:
+    batch = src.numel() // (K * N)
+    _abi.call("pi0hip_pack_weight", _ptr(src), _ptr(dst), K, N, batch, _stream())
+
+
+def packed_weight_ptr(w: torch.Tensor) -> int:
+    """Device address of the packed copy of `w` ([K, N] bf16, possibly a layer view)."""
+    _check(w, "weight", 2)
+    if not w.is_contiguous():
+        raise ValueError("weight must be contiguous [K, N]")
+    K, N = w.shape
+    ptr = w.data_ptr()
+    for e in _PACKED:
+        if e.K == K and e.N == N and e.base <= ptr < e.base + e.nbytes:
+            if not _capturing() and e.version != e.src._version:
+                _pack_into(e.src, e.packed, K, N)
+                e.version = e.src._version
+            return e.packed.data_ptr() + (ptr - e.base)
+    if _capturing():
+        raise RuntimeError("weight was not packed before graph capture; run a warmup pass first")
+    base = w._base if w._base is not None else w
+    src = base if (base.dim() >= 2 and base.is_contiguous() and tuple(base.shape[-2:]) == (K, N)
+                   and base.dtype == w.dtype) else w
+    packed = torch.empty_like(src)
+    _pack_into(src, packed, K, N)
+    entry = _PackedEntry(src, packed, K, N)
+    _PACKED.append(entry)
+    return packed.data_ptr() + (ptr - entry.base)
+
+
+def prepare_weights(weights: dict) -> None:
+    """Pack every 2-D/3-D GEMM weight of the decoder up front (outside any capture)."""
+    for name in ("decoder_action_mlp_w", "decoder_attn_qkv_w", "decoder_attn_o_w",
+                 "decoder_ffn_gate_w", "decoder_ffn_up_w", "decoder_ffn_down_w",
+                 "decoder_action_fused_out_proj_w"):
+        if name in weights:
+            w = weights[name]
+            packed_weight_ptr(w if w.dim() == 2 else w[0])
+
+
+def clear_packed_cache() -> None:
+    _PACKED.clear()
+
+
+def _splitk(M: int, N: int, K: int, target: int = 256) -> int:
+    """Split K across workgroups until the grid covers the 256 CUs (K per wave stays >= 32)."""
+    tiles = ((M + 63) // 64) * (N // 16)
+    kt = K // 32
+    s = 1
+    while tiles * s < target and kt % (4 * s * 2) == 0:
+        s *= 2
+    return s
+
+
+def _gemm_ws(role: str, M: int, N: int, splitk: int, dual: int, device):
+    nbytes = _abi.lib().pi0hip_gemm_workspace_bytes(M, N, splitk, dual)
+    if nbytes == 0:
+        return None, 0
+    buf = scratch(role, (nbytes,), torch.uint8, device)
+    return buf.data_ptr(), nbytes
+
+
+# ---------------------------------------------------------------------------
+# Decoder call sites (pipeline.py:92-135 calls these by name)
+# ---------------------------------------------------------------------------
+def decoder_state_proj(x, weight, bias, out):
+    """out = x @ weight + bias for the state token (wrappers.py:108-112)."""
+    _check(x, "x"); _check(weight, "weight", 2); _check(bias, "bias", 1); _check(out, "out", 2)
+    K, N = weight.shape
+    if x.numel() != K or out.shape != (1, N) or bias.shape != (N,):
+        raise ValueError("decoder_state_proj: shape mismatch")
+    _abi.call("pi0hip_small_linear", _ptr(x), K, _ptr(weight), _ptr(bias), _ptr(out),
+              out.stride(0), 1, N, K, 0, _stream())
+    return out
+
+
+def decoder_action_in_proj(x, weight, bias, out):
+    """out = silu(x @ weight + bias) (wrappers.py:115-120)."""
+    _check(x, "x", 2); _check(weight, "weight", 2); _check(bias, "bias", 1); _check(out, "out", 2)
+    M, K = x.shape
+    N = weight.shape[1]
+    if weight.shape[0] != K or out.shape != (M, N) or bias.shape != (N,):
+        raise ValueError("decoder_action_in_proj: shape mismatch")
+    _abi.call("pi0hip_small_linear", _ptr(x), x.stride(0), _ptr(weight), _ptr(bias), _ptr(out),
+              out.stride(0), M, N, K, 1, _stream())
+    return out
+
+
+def decoder_action_mlp(x, weight, bias, out):
+    """out = x @ weight + bias, out = decoder_x[1:] (wrappers.py:123-128)."""
+    _check(x, "x", 2); _check(bias, "bias", 1); _check(out, "out", 2)
+    M, K = x.shape
+    N = weight.shape[1]
+    if weight.shape[0] != K or out.shape != (M, N) or bias.shape != (N,):
+        raise ValueError("decoder_action_mlp: shape mismatch")
+    wp = packed_weight_ptr(weight)
+    s = _splitk(M, N, K)
+    ws, nbytes = _gemm_ws("gemm_ws_mlp", M, N, s, 0, x.device)
+    _abi.call("pi0hip_linear_bias", _ptr(x), x.stride(0), wp, _ptr(bias), _ptr(out),
+              out.stride(0), M, N, K, s, ws, nbytes, _stream())
+    return out
+
+
+def decoder_norm_qkv_rope(x, weight_qkv, rope, Q, K, V, norm_factor):
+    """RMS factor, QKV projection, RoPE, scatter into Q and the K/V cache rows (wrappers.py:131-144)."""
+    _check(x, "x", 2); _check(rope, "rope", 2); _check(Q, "Q", 2)
+    _check(K, "K", 2); _check(V, "V", 2)
+    M, Kdim = x.shape
+    head_dim = V.shape[1]
+    heads = Q.shape[0] // M
+    if (Q.shape != (M * heads, head_dim) or not Q.is_contiguous() or K.shape != (M, head_dim)
+            or V.shape != (M, head_dim) or K.stride(0) != V.stride(0)
+            or weight_qkv.shape != (Kdim, (heads + 2) * head_dim)
+            or rope.shape != (M, head_dim) or not rope.is_contiguous()):
+        raise ValueError("decoder_norm_qkv_rope: shape mismatch")
+    nf = 0
+    if norm_factor is not None:
+        _check(norm_factor, "norm_factor", 1)
+        if norm_factor.shape[0] < M:
+            raise ValueError("norm_factor too short")
+        nf = _ptr(norm_factor)
+    wp = packed_weight_ptr(weight_qkv)
+    _abi.call("pi0hip_norm_qkv_rope", _ptr(x), x.stride(0), wp, _ptr(rope), _ptr(Q), _ptr(K),
+              _ptr(V), K.stride(0), nf, M, Kdim, heads, head_dim, _stream())
+
+
+def decoder_attention(Q, K, V, scores, out, encoder_seq_len):
+    """Masked single-KV-head attention; `out` may be `Q`, `scores` is unused (fused_wrappers.py:88-115)."""
+    _check(Q, "Q", 2); _check(K, "K", 2); _check(V, "V", 2); _check(out, "out", 2)
+    rows, head_dim = Q.shape
+    keys = K.shape[0]
+    if V.shape != K.shape or K.shape[1] != head_dim or out.shape != Q.shape \
+            or K.stride(0) != V.stride(0):
+        raise ValueError("decoder_attention: shape mismatch")
+    lib = _abi.lib()
+    nbytes = lib.pi0hip_attention_workspace_bytes(rows, keys)
+    ws = scratch("attn_ws", (nbytes,), torch.uint8, Q.device)
+    _abi.call("pi0hip_attention", _ptr(Q), Q.stride(0), _ptr(K), _ptr(V), K.stride(0), _ptr(out),
+              out.stride(0), rows, keys, int(encoder_seq_len), DECODER_HEADS, head_dim,
+              ws.data_ptr(), nbytes, _stream())
+    return out
+
+
+def _residual(x, weight, out, role):
+    _check(x, "x", 2); _check(out, "out", 2)
+    M, K = x.shape
+    N = weight.shape[1]
+    if weight.shape[0] != K or out.shape != (M, N):
+        raise ValueError(f"{role}: shape mismatch")
+    wp = packed_weight_ptr(weight)
+    s = _splitk(M, N, K)
+    ws, nbytes = _gemm_ws(f"gemm_ws_{role}", M, N, s, 0, x.device)
+    _abi.call("pi0hip_linear_residual", _ptr(x), x.stride(0), wp, _ptr(out), out.stride(0),
+              M, N, K, s, ws, nbytes, _stream())
+    return out
+
+
+def decoder_out_proj_residual(x, weight, out):
+    """out += x @ weight (wrappers.py:176-181)."""
+    return _residual(x, weight, out, "o_proj")
+
+
+def decoder_ffn_down_residual(x, weight, out):
+    """out += x @ weight (wrappers.py:184-189)."""
+    return _residual(x, weight, out, "ffn_down")
+
+
+def _gated_ffn(x, gate_w, up_w, out):
+    _check(x, "x", 2); _check(out, "out", 2)
+    M, K = x.shape
+    N = gate_w.shape[1]
+    if gate_w.shape != (K, N) or up_w.shape != (K, N) or out.shape != (M, N):
+        raise ValueError("decoder_norm_gated_ffn: shape mismatch")
+    gp = packed_weight_ptr(gate_w)
+    up = packed_weight_ptr(up_w)
+    _abi.call("pi0hip_norm_gated_ffn", _ptr(x), x.stride(0), gp, up, _ptr(out), out.stride(0),
+              M, N, K, _stream())
+    return out
+
+
+def decoder_norm_gated_ffn(x, gate_w, up_w, out, norm_factor):
+    """out = gelu(f * x@Wg) * (f * x@Wu), f computed in-kernel (fused_norm.py:26-78)."""
+    return _gated_ffn(x, gate_w, up_w, out)
+
+
+def _action_out(x, weight, bias, out):
+    _check(x, "x", 2); _check(bias, "bias", 1); _check(out, "out", 2)
+    M, K = x.shape
+    N = weight.shape[1]
+    if weight.shape[0] != K or out.shape != (M, N) or bias.shape != (N,):
+        raise ValueError("decoder_action_out_proj: shape mismatch")
+    wp = packed_weight_ptr(weight)
+    s = _splitk(M, N, K)
+    ws, nbytes = _gemm_ws("gemm_ws_out", M, N, s, 0, x.device)
+    _abi.call("pi0hip_rms_linear_bias_residual", _ptr(x), x.stride(0), wp, _ptr(bias), _ptr(out),
+              out.stride(0), M, N, K, s, ws, nbytes, _stream())
+    return out
+
+
+def decoder_action_out_proj(x, weight, bias, out, norm_factor):
+    """Euler update out += bias + f * x@W (fused_norm.py:81-125); `norm_factor` untouched."""
+    return _action_out(x, weight, bias, out)
+
+
+DECODER_WRAPPERS = {
+    "decoder_state_proj": decoder_state_proj,
+    "decoder_action_in_proj": decoder_action_in_proj,
+    "decoder_action_mlp": decoder_action_mlp,
+    "decoder_norm_qkv_rope": decoder_norm_qkv_rope,
+    "decoder_attention": decoder_attention,
+    "decoder_out_proj_residual": decoder_out_proj_residual,
+    "decoder_ffn_down_residual": decoder_ffn_down_residual,
+    "decoder_norm_gated_ffn": decoder_norm_gated_ffn,
+    "decoder_action_out_proj": decoder_action_out_proj,
+}
+
+ALL_WRAPPERS = dict(DECODER_WRAPPERS)

@@ -1,0 +1,56 @@
+"""Static decoder buffers and the RoPE table (mirrors `hardware/nvidia/h100/pi0/buffers.py`).
+
+Layout in HBM (all bf16, row-major, allocated once; the hot loop only writes
+in place):
+  encoder_K / encoder_V  [18, enc_len + chunk + 1, 256]  prefix rows then decoder rows
+  decoder_x              [chunk + 1, 1024]               residual stream (row 0 = state)
+  decoder_q_buf          [(chunk + 1) * 8, 256]          flat (token * 8 + head) queries,
+                                                         reused as the attention output
+  decoder_hidden         [chunk + 1, 4096]               GeGLU activations
+"""
+from __future__ import annotations
+
+import torch
+
+from .spec import DECODER_FFN, DECODER_HEADS, DECODER_LAYERS, DECODER_WIDTH, HEAD_DIM, ROPE_THETA
+
+
+def rope_table(seq_len: int, offset: int, head_dim: int, device) -> torch.Tensor:
+    """Interleaved (cos, sin) bf16 table for positions [offset, offset + seq_len) (buffers.py:15-23)."""
+    positions = torch.arange(seq_len, device=device) + offset
+    inv_freq = 1.0 / (ROPE_THETA ** (torch.arange(0, head_dim, 2, dtype=torch.float32,
+                                                  device=device) / head_dim))
+    phase = inv_freq[None, :] * positions[:, None]
+    cos = torch.cos(phase).to(torch.bfloat16)
+    sin = torch.sin(phase).to(torch.bfloat16)
+    return torch.cat([cos[:, :, None], sin[:, :, None]], 2).view(-1, head_dim)
+
+
+def allocate_decoder_buffers(encoder_seq_len: int, chunk_size: int, device,
+                             layers: int = DECODER_LAYERS, width: int = DECODER_WIDTH,
+                             ffn: int = DECODER_FFN, heads: int = DECODER_HEADS,
+                             head_dim: int = HEAD_DIM, action_dim: int = 32) -> dict:
+    """Every persistent buffer the decoder loop touches (buffers.py:37-64, decoder part)."""
+    bf16 = torch.bfloat16
+    dec_len = chunk_size + 1
+    cache_len = encoder_seq_len + dec_len
+
+    def buf(*shape, dtype=bf16):
+        return torch.zeros(shape, dtype=dtype, device=device)
+
+    buffers = {
+        "observation_state_normalized": buf(action_dim),
+        "diffusion_noise": buf(chunk_size, action_dim),
+        "encoder_K": buf(layers, cache_len, head_dim),
+        "encoder_V": buf(layers, cache_len, head_dim),
+        "decoder_rope_weights": buf(dec_len, head_dim),
+        "decoder_x": buf(dec_len, width),
+        "decoder_x_buf": buf(chunk_size, width),
+        "decoder_state_buf": buf(1, width),
+        "decoder_norm_factor_buf": buf(dec_len),
+        "decoder_q_buf": buf(dec_len * heads, head_dim),
+        "decoder_attn_buf": buf(dec_len * heads, cache_len),
+        "decoder_hidden": buf(dec_len, ffn),
+    }
+    buffers["decoder_rope_weights"].copy_(rope_table(dec_len, encoder_seq_len, head_dim, device))
+    return buffers

@@ -1,0 +1,114 @@
+"""Engines: static buffers + one hipGraph for the Pi0 denoising loop.
+
+`Pi0DecoderEngine` mirrors the capture discipline of the reference's
+`Pi0Inference` (`hardware/nvidia/h100/pi0/engine.py:26-86`): allocate every
+buffer up front, copy weights in, warm up (which also fills the scratch pool
+and the packed-weight cache), freeze the pool, capture one graph on a side
+stream; `forward` copies the inputs into their static buffers and replays.
+The prefix KV cache (the encoder's output) is supplied by the caller through
+`load_prefix`; the vision and prefix-encoder stages are not part of this
+engine.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import pipeline
+from .arena import ScratchPool
+from .backends import BACKENDS
+from .buffers import allocate_decoder_buffers
+from .ops import op_table
+from .spec import DECODER_WEIGHT_NAMES, decoder_weight_shapes
+
+
+class Pi0DecoderEngine:
+    """The captured 10-step decoder loop against a caller-supplied prefix KV cache.
+
+    steps and layers exist for bisection, as in the reference engine.
+    """
+
+    def __init__(self, weights: dict, encoder_seq_len: int = 768, chunk_size: int = 50,
+                 steps: int = 10, layers: int = 18, fused: bool = True, backend: str = "hip",
+                 plan: dict | None = None, device: str = "cuda", capture: bool = True,
+                 warmup: int = 3):
+        self.encoder_seq_len = encoder_seq_len
+        self.chunk_size = chunk_size
+        self.steps = steps
+        self.layers = layers
+        self.ops = op_table(fused, backend=backend, plan=plan)
+        self.backend = BACKENDS[backend]
+        n_layers = weights["decoder_attn_qkv_w"].shape[0]
+        if layers > n_layers:
+            raise ValueError(f"layers={layers} but the checkpoint has {n_layers}")
+        dims = _dims_from(weights)
+        expected = decoder_weight_shapes(n_layers, **dims)
+        self.weights = {}
+        for name in DECODER_WEIGHT_NAMES:
+            w = weights[name]
+            if tuple(w.shape) != expected[name]:
+                raise ValueError(f"{name}: shape {tuple(w.shape)}, expected {expected[name]}")
+            self.weights[name] = torch.empty(expected[name], dtype=torch.bfloat16, device=device)
+            self.weights[name].copy_(w)
+        self.buffers = allocate_decoder_buffers(
+            encoder_seq_len, chunk_size, device, layers=n_layers, width=dims["width"],
+            ffn=dims["ffn"], heads=dims["heads"], head_dim=dims["head_dim"],
+            action_dim=dims["action_dim"])
+        self.pool = ScratchPool()
+        self.graph = None
+        if hasattr(self.backend, "prepare_weights"):
+            self.backend.prepare_weights(self.weights)
+        if capture:
+            self._capture(warmup)
+
+    def _run(self):
+        with self.backend.use_pool(self.pool):
+            pipeline.transformer_decoder(self.ops, self.weights, self.buffers,
+                                         self.encoder_seq_len, steps=self.steps,
+                                         layers=self.layers)
+
+    def _capture(self, warmup: int):
+        saved = self.buffers["diffusion_noise"].clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                self._run()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self.pool.freeze()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._run()
+        torch.cuda.synchronize()
+        self.buffers["diffusion_noise"].copy_(saved)
+
+    def load_prefix(self, prefix_k: torch.Tensor, prefix_v: torch.Tensor) -> None:
+        """Copy the prefix K/V ([layers, >= enc_len, head_dim]) into the static cache."""
+        e = self.encoder_seq_len
+        self.buffers["encoder_K"][:, :e].copy_(prefix_k[:, :e])
+        self.buffers["encoder_V"][:, :e].copy_(prefix_v[:, :e])
+
+    def forward(self, state: torch.Tensor, noise: torch.Tensor) -> torch.Tensor:
+        """Denoise one action chunk; returns the static `diffusion_noise` buffer."""
+        self.buffers["observation_state_normalized"].copy_(state)
+        self.buffers["diffusion_noise"].copy_(noise)
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self._run()
+        return self.buffers["diffusion_noise"]
+
+    def replay(self) -> None:
+        self.graph.replay()
+
+
+def _dims_from(weights: dict) -> dict:
+    qkv = weights["decoder_attn_qkv_w"]
+    o = weights["decoder_attn_o_w"]
+    width = qkv.shape[1]
+    qkv_n = qkv.shape[2]
+    q_dim = o.shape[1]
+    head_dim = (qkv_n - q_dim) // 2
+    return dict(width=width, ffn=weights["decoder_ffn_gate_w"].shape[2], heads=q_dim // head_dim,
+                head_dim=head_dim, action_dim=weights["decoder_state_in_proj_w"].shape[0],
+                steps=weights["decoder_action_fused_time_biases"].shape[0])

@@ -1,0 +1,102 @@
+/*
+ * C ABI of libpi0hip.so: hand-written gfx950 (MI355X) kernels for the Pi0
+ * action-expert denoising loop.
+ *
+ * Every entry point takes plain device pointers, element counts / leading
+ * dimensions (in elements), an optional workspace and a hipStream_t. All
+ * tensors are bf16 row-major unless stated. Launches are asynchronous, never
+ * synchronise and never allocate, so they can be recorded into a hipGraph.
+ * Return value: 0 on success, a negative PI0HIP_ERR_* for a rejected
+ * argument (nothing launched), or a positive hipError_t from the launch.
+ *
+ * Weights named `*_packed` are in the B-fragment layout written by
+ * pi0hip_pack_weight (one-time, outside the hot loop).
+ *
+ * Each entry point replaces the reference call site named in its comment
+ * (paths relative to src/flash_vla/hardware/nvidia/h100/pi0/backends/tilelang/).
+ */
+#ifndef PI0_HIP_H
+#define PI0_HIP_H
+
+#include <stddef.h>
+#include <hip/hip_runtime.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PI0HIP_ERR_ARG (-1)        /* null pointer, non-positive size, bad enum */
+#define PI0HIP_ERR_SHAPE (-2)      /* shape the kernels do not support         */
+#define PI0HIP_ERR_WORKSPACE (-3)  /* workspace missing or too small           */
+
+/* Library version: 100 * major + minor. */
+int pi0hip_version(void);
+
+/* W[batch][K][N] -> B-fragment packed copy of the same size. K % 32 == 0, N % 16 == 0.
+ * Replaces nothing in the reference (TileLang reads the [K, N] weights through
+ * TMA); this is the one-time relayout that makes the weight stream coalesced. */
+int pi0hip_pack_weight(const void* w, void* packed, int K, int N, int batch, hipStream_t s);
+
+/* Workspace for the split-K GEMMs (0 when splitk == 1). Counters inside must
+ * start zeroed; the kernels leave them zeroed again. */
+size_t pi0hip_gemm_workspace_bytes(int M, int N, int splitk, int dual);
+
+/* out[m, n] = act(x[m, :K] @ w[K, N] + bias[n]); act 0 = identity, 1 = silu.
+ * Unpacked w; for K = 32 projections.
+ * decoder_state_proj     wrappers.py:108-112 (tl_matmul_bias, kernels/base.py:158-192)
+ * decoder_action_in_proj wrappers.py:115-120 (tl_matmul_bias_silu, kernels/base.py:304-335) */
+int pi0hip_small_linear(const void* x, int ldx, const void* w, const void* bias, void* out,
+                        int ldo, int M, int N, int K, int act, hipStream_t s);
+
+/* out = x @ W + bias, fp32 accumulation, M <= 64 per 64-row block.
+ * decoder_action_mlp wrappers.py:123-128 (tl_matmul_bias, kernels/base.py:158-192) */
+int pi0hip_linear_bias(const void* x, int ldx, const void* w_packed, const void* bias, void* out,
+                       int ldo, int M, int N, int K, int splitk, void* ws, size_t ws_bytes,
+                       hipStream_t s);
+
+/* out += x @ W (in place, one bf16 rounding).
+ * decoder_out_proj_residual wrappers.py:176-181, decoder_ffn_down_residual
+ * wrappers.py:184-189 (tl_matmul_res, kernels/base.py:115-154) */
+int pi0hip_linear_residual(const void* x, int ldx, const void* w_packed, void* out, int ldo,
+                           int M, int N, int K, int splitk, void* ws, size_t ws_bytes,
+                           hipStream_t s);
+
+/* out += bias + f * (x @ W), f[m] = bf16(rsqrt(mean(x[m]^2) + 1e-6)).
+ * decoder_action_out_proj fused_wrappers.py:57-67 (tl_fused_rms_matmul_bias_res,
+ * kernels/fused_norm.py:81-125) */
+int pi0hip_rms_linear_bias_residual(const void* x, int ldx, const void* w_packed,
+                                    const void* bias, void* out, int ldo, int M, int N, int K,
+                                    int splitk, void* ws, size_t ws_bytes, hipStream_t s);
+
+/* acc = f * (x @ Wqkv), RoPE on adjacent pairs of the first (heads+1)*head_dim
+ * columns with rope[m] = interleaved bf16 (cos, sin); scatter to
+ * q [M, heads*head_dim], k/v rows [M, ldkv]; norm_factor[m] = f (optional, may be NULL).
+ * decoder_norm_qkv_rope wrappers.py:131-144 (tl_rms_factor + tl_qkv_gemm_rope,
+ * kernels/base.py:344-370, 607-669) */
+int pi0hip_norm_qkv_rope(const void* x, int ldx, const void* w_packed, const void* rope, void* q,
+                         void* k, void* v, int ldkv, void* norm_factor, int M, int K, int heads,
+                         int head_dim, hipStream_t s);
+
+/* out = gelu_tanh(f * (x @ Wg)) * (f * (x @ Wu)), f from x in-kernel.
+ * decoder_norm_gated_ffn fused_wrappers.py:45-54 (tl_fused_rms_gate,
+ * kernels/fused_norm.py:26-78) */
+int pi0hip_norm_gated_ffn(const void* x, int ldx, const void* gate_packed, const void* up_packed,
+                          void* out, int ldo, int M, int N, int K, hipStream_t s);
+
+/* Workspace for pi0hip_attention. */
+size_t pi0hip_attention_workspace_bytes(int rows, int keys);
+
+/* out = softmax(mask(q k^T / sqrt(head_dim))) v over `keys` cache rows; flat
+ * query row r = token * heads + head; rows r < heads keep keys j <= enc_len.
+ * `out` may alias `q`. head_dim must be 256.
+ * decoder_attention fused_wrappers.py:88-115 (tl_fd_flat_split + tl_fd_flat_combine,
+ * kernels/base.py:801-923) */
+int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int ldkv, void* out,
+                     int ldo, int rows, int keys, int enc_len, int heads, int head_dim,
+                     void* ws, size_t ws_bytes, hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PI0_HIP_H */
