@@ -52,6 +52,46 @@ __device__ __forceinline__ float gelu_tanh(float v) {
 }
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
 
+// ---- device-coherent exchange between workgroups of one launch ---------------
+// On gfx950 every XCD has its own L2, and plain stores/loads are not coherent
+// across XCDs inside a kernel. Agent-scope fences (an L2 writeback or
+// invalidate) cost microseconds, so cross-workgroup data instead travels with
+// device-scope (sc1) stores and loads, which go to the memory-side coherence
+// point, and the producer waits for its stores to complete before it signals.
+__device__ __forceinline__ void store_dev4(float* p, f32x4 v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void store_dev1(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev1(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Four device-scope dword loads the compiler can keep in flight together.
+__device__ __forceinline__ f32x4 load_dev4(const float* p) {
+  f32x4 v;
+  v[0] = load_dev1(p); v[1] = load_dev1(p + 1); v[2] = load_dev1(p + 2); v[3] = load_dev1(p + 3);
+  return v;
+}
+// Wait until every vector memory operation of this wave has completed.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Arrival counter for "last workgroup finishes": every thread has issued its
+// device-scope stores; returns true (in all threads) for the last of `total`
+// arrivals, which also resets the counter for the next launch.
+__device__ __forceinline__ bool arrive_last(int* counter, int total, int* s_flag) {
+  wait_vmem();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = prev == total - 1;
+    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *s_flag = last;
+  }
+  __syncthreads();
+  return *s_flag != 0;
+}
+
 __device__ __forceinline__ float warp_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, PI0_WAVE);

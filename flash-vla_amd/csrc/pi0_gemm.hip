@@ -150,36 +150,25 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
     float* ssp = a.ws + part_floats((int)tiles, splitk, ND);
     {
       float* p = part + (((size_t)tile * splitk + ks) * 64 + lrow) * 16 * ND + c4;
-      *reinterpret_cast<f32x4*>(p) = f32x4{v0[0], v0[1], v0[2], v0[3]};
-      if constexpr (DUAL) *reinterpret_cast<f32x4*>(p + 16) = f32x4{v1[0], v1[1], v1[2], v1[3]};
-      if (RMS && (t & 3) == 0) ssp[((size_t)tile * splitk + ks) * 64 + lrow] = ss;
+      store_dev4(p, f32x4{v0[0], v0[1], v0[2], v0[3]});
+      if constexpr (DUAL) store_dev4(p + 16, f32x4{v1[0], v1[1], v1[2], v1[3]});
+      if (RMS && (t & 3) == 0) store_dev1(ssp + ((size_t)tile * splitk + ks) * 64 + lrow, ss);
     }
-    __threadfence();
-    __syncthreads();
-    if (t == 0) {
-      const int prev = atomicAdd(&a.counters[tile], 1);
-      const int last = prev == splitk - 1;
-      if (last) atomicExch(&a.counters[tile], 0);
-      __threadfence();
-      s_last = last;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+    if (!arrive_last(a.counters + tile, splitk, &s_last)) return;
 #pragma unroll
     for (int c = 0; c < 4; ++c) { v0[c] = 0.f; v1[c] = 0.f; }
     ss = 0.f;
     for (int k = 0; k < splitk; ++k) {
       const float* p = part + (((size_t)tile * splitk + k) * 64 + lrow) * 16 * ND + c4;
-      const f32x4 q0 = *reinterpret_cast<const f32x4*>(p);
+      const f32x4 q0 = load_dev4(p);
 #pragma unroll
       for (int c = 0; c < 4; ++c) v0[c] += q0[c];
       if constexpr (DUAL) {
-        const f32x4 q1 = *reinterpret_cast<const f32x4*>(p + 16);
+        const f32x4 q1 = load_dev4(p + 16);
 #pragma unroll
         for (int c = 0; c < 4; ++c) v1[c] += q1[c];
       }
-      if constexpr (RMS) ss += ssp[((size_t)tile * splitk + k) * 64 + lrow];
+      if constexpr (RMS) ss += load_dev1(ssp + ((size_t)tile * splitk + k) * 64 + lrow);
     }
   }
 

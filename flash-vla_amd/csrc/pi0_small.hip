@@ -1,5 +1,6 @@
 // Projections from the 32-wide action/state space (K = 32): far too small for
-// MFMA tiling to matter, so one thread computes one output element in fp32.
+// MFMA tiling to matter. One thread computes 8 adjacent outputs of one row in
+// fp32 from 16-byte weight loads, all K rows of loads in flight at once.
 //   decoder_state_proj      out = x @ W + b          (wrappers.py:108-112)
 //   decoder_action_in_proj  out = silu(x @ W + b)    (wrappers.py:115-120)
 #include "pi0_common.h"
@@ -7,18 +8,32 @@
 
 namespace pi0 {
 
+template <int K>
 __global__ __launch_bounds__(256) void small_k_linear_kernel(
     const __bf16* __restrict__ x, int ldx, const __bf16* __restrict__ w,
-    const __bf16* __restrict__ bias, __bf16* __restrict__ out, int ldo, int M, int N, int K,
-    int act) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  const int m = blockIdx.y;
-  if (n >= N || m >= M) return;
-  float acc = 0.f;
-  for (int k = 0; k < K; ++k) acc += bf2f(x[(size_t)m * ldx + k]) * bf2f(w[(size_t)k * N + n]);
-  acc += bf2f(bias[n]);
-  if (act == 1) acc = silu(acc);
-  out[(size_t)m * ldo + n] = f2bf(acc);
+    const __bf16* __restrict__ bias, __bf16* __restrict__ out, int ldo, int M, int N, int act) {
+  const int groups = N / 8;
+  const int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= M * groups) return;
+  const int m = id / groups, n = (id - m * groups) * 8;
+  bf16x8 wv[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) wv[k] = load8(w + (size_t)k * N + n);
+  float xv[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) xv[k] = bf2f(x[(size_t)m * ldx + k]);
+  const bf16x8 bv = load8(bias + n);
+  bf16x8 o;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float acc = 0.f;
+#pragma unroll
+    for (int k = 0; k < K; ++k) acc += xv[k] * bf2f(wv[k][j]);
+    acc += bf2f(bv[j]);
+    if (act == 1) acc = silu(acc);
+    o[j] = f2bf(acc);
+  }
+  *reinterpret_cast<bf16x8*>(out + (size_t)m * ldo + n) = o;
 }
 
 }  // namespace pi0
@@ -28,8 +43,10 @@ extern "C" int pi0hip_small_linear(const void* x, int ldx, const void* w, const 
                                    hipStream_t s) {
   if (!x || !w || !bias || !out || M <= 0 || N <= 0 || K <= 0) return PI0HIP_ERR_ARG;
   if (act != 0 && act != 1) return PI0HIP_ERR_ARG;
-  dim3 grid((N + 255) / 256, M);
-  hipLaunchKernelGGL(pi0::small_k_linear_kernel, grid, dim3(256), 0, s, (const __bf16*)x, ldx,
-                     (const __bf16*)w, (const __bf16*)bias, (__bf16*)out, ldo, M, N, K, act);
+  if (N % 8 || K != 32 || ldo % 8) return PI0HIP_ERR_SHAPE;
+  const int threads = M * (N / 8);
+  hipLaunchKernelGGL(pi0::small_k_linear_kernel<32>, dim3((threads + 255) / 256), dim3(256), 0, s,
+                     (const __bf16*)x, ldx, (const __bf16*)w, (const __bf16*)bias, (__bf16*)out,
+                     ldo, M, N, act);
   return (int)hipGetLastError();
 }

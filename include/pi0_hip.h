@@ -42,7 +42,7 @@ int pi0hip_pack_weight(const void* w, void* packed, int K, int N, int batch, hip
 size_t pi0hip_gemm_workspace_bytes(int M, int N, int splitk, int dual);
 
 /* out[m, n] = act(x[m, :K] @ w[K, N] + bias[n]); act 0 = identity, 1 = silu.
- * Unpacked w; for K = 32 projections.
+ * Unpacked w; K must be 32, N and ldo multiples of 8.
  * decoder_state_proj     wrappers.py:108-112 (tl_matmul_bias, kernels/base.py:158-192)
  * decoder_action_in_proj wrappers.py:115-120 (tl_matmul_bias_silu, kernels/base.py:304-335) */
 int pi0hip_small_linear(const void* x, int ldx, const void* w, const void* bias, void* out,
