@@ -34,6 +34,9 @@ KV_WRITE_BYTES = LAYERS * 51 * 256 * 2 * 2
 STEP_BYTES = LAYERS * LAYER_WEIGHT_BYTES + SMALL_PROJ_BYTES + KV_READ_BYTES + KV_WRITE_BYTES
 CHUNK_BYTES = STEPS * STEP_BYTES           # 6,411,223,680 B
 GATE_BYTES = 2 * 1024 * 4096 * 2           # gate + up weights of one layer (activations excluded)
+# HBM bytes per launch of the gate kernel from rocprofv3 FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0
+# (factors from a plain 256 MiB copy); profiles/decoder_kernels_config2_hbm_traffic.md
+GATE_TRAFFIC_BYTES = (8685.5 * 2.0 + 408.0 * 1.0) * 1024
 
 
 def _time_graph(run, n_inner, reps, torch):
@@ -73,7 +76,7 @@ def kernel_roofline(eng, torch):
     achieved = GATE_BYTES / (us * 1e-6) / 1e9
     return {"kernel": "skinny_gemm_kernel<EPI_GATE> (decoder_norm_gated_ffn)",
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": int(GATE_TRAFFIC_BYTES),
             "avg_launch_us": round(us, 3), "bytes_per_launch": GATE_BYTES}
 
 
@@ -110,6 +113,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-kernel", action="store_true", help="skip the per-kernel roofline leg")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MiB device copy (5x), to calibrate rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE against a kernel of known traffic")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the decoder loop is a single-GPU path); "
@@ -117,6 +123,16 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calibration:
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": src.numel() * 4,
+                          "copy_calibration_bytes_written": dst.numel() * 4, "launches": 5}))
+        return
+
     from flash_vla_amd import Pi0DecoderEngine
     from flash_vla_amd.weights import decoder_checkpoint, decoder_inputs
 

@@ -4,30 +4,33 @@
 //   o = softmax(mask(Q K^T / sqrt(256))) V, where flat rows < heads (the state
 //   token) keep keys j <= enc_len and every other row keeps all keys.
 //
-// One kernel. Workgroup = 16 query rows x 128 keys; its 4 waves take 32 keys
-// each (flash-decoding inside the workgroup):
-//   * S^T = K Q^T with K rows as the MFMA A operand and Q rows as B, both read
-//     straight from global memory in fragment order. In the S^T accumulator a
-//     lane holds, for one query row, keys {4g..4g+3} of each 16-key tile --
-//     exactly the A-operand layout P @ V needs once the MFMA's key slots are
-//     permuted the same way in the V fragment, so P never leaves registers.
-//   * V (row-major, 256 columns per key) is transposed into LDS on the way in
-//     so that the B fragment (4 + 4 keys of one column) is two 8-byte reads.
-//   * log2-domain softmax per wave, merged across the 4 waves through LDS,
-//     P rounded to bf16 before P @ V as in the reference.
+// One kernel. Workgroup = 16 query rows x 128 keys:
+//   * K, V (128 rows) and Q (16 rows) are staged in LDS with coalesced
+//     16-byte loads (row pitch padded by 16 bytes so fragment reads are free
+//     of bank conflicts);
+//   * each of the 4 waves takes 32 keys (flash-decoding inside the
+//     workgroup): S^T = K Q^T with K rows as the MFMA A operand and Q rows as
+//     B. In the S^T accumulator a lane holds, for one query row, keys
+//     {4g..4g+3} of each 16-key tile -- the A-operand layout P @ V needs once
+//     the MFMA's key slots are permuted the same way in the V fragment, so P
+//     never leaves registers;
+//   * log2-domain softmax per wave (lane shuffles), merged across the 4 waves
+//     through LDS; P is rounded to bf16 before P @ V as in the reference.
 // When the keys span several chunks, each workgroup writes its normalised
-// partial O and log2-sum-exp with device-scope stores; the last workgroup of
-// a query tile (arrival counter) merges them in chunk order and writes O.
+// partial O and log2-sum-exp with coalesced device-scope stores; the last
+// workgroup of a query tile (arrival counter) merges them in chunk order.
 #include "pi0_common.h"
 #include "pi0_hip.h"
 
 namespace pi0 {
 
 constexpr int ATT_HD = 256;
-constexpr int ATT_QT = 16;     // query rows per workgroup
-constexpr int ATT_CH = 128;    // keys per workgroup (32 per wave)
-constexpr int VT_P = 40;       // bf16 pitch of a transposed-V row (32 keys + pad)
+constexpr int ATT_QT = 16;          // query rows per workgroup
+constexpr int ATT_CH = 128;         // keys per workgroup (32 per wave)
+constexpr int KP = ATT_HD + 8;      // bf16 pitch of staged K / V / Q rows
+constexpr int OBP = ATT_HD + 4;     // fp32 pitch of the per-wave O buffer
 constexpr float NEG_BIG = -1.0e30f;
+constexpr int MAX_CHUNKS = 8;       // keys <= 1024
 
 struct AttnArgs {
   const __bf16* q; int ldq;
@@ -39,67 +42,72 @@ struct AttnArgs {
 };
 
 __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
-  // vt: per-wave transposed V slice; reused as the per-wave O buffer after P @ V.
-  __shared__ __attribute__((aligned(16))) __bf16 vt[4][ATT_HD][VT_P];
+  __shared__ __attribute__((aligned(16))) __bf16 ks_[ATT_CH][KP];   // reused as O buffer
+  __shared__ __attribute__((aligned(16))) __bf16 vs_[ATT_CH][KP];
+  __shared__ __attribute__((aligned(16))) __bf16 qs_[ATT_QT][KP];
   __shared__ float sm[4][ATT_QT], sl[4][ATT_QT];
   __shared__ int s_last;
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int qt = blockIdx.x, c = blockIdx.y;
-  const int q0 = qt * ATT_QT;
-  const int kw0 = c * ATT_CH + wave * 32;            // first key of this wave
+  const int q0 = qt * ATT_QT, k0 = c * ATT_CH;
 
-  // ---- issue global loads: V slice (for LDS), K fragments (A), Q fragments (B)
-  bf16x8 vreg[16];
-#pragma unroll
-  for (int p = 0; p < 16; ++p) {
-    const int key = kw0 + (lane & 31);
-    const int d = (p * 2 + (lane >> 5)) * 8;
-    vreg[p] = key < a.keys ? load8(a.v + (size_t)key * a.ldkv + d) : zero8();
-  }
-  bf16x8 kf[2][8], qf[8];
-#pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int key = kw0 + nt * 16 + r;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-      kf[nt][ks] = key < a.keys ? load8(a.k + (size_t)key * a.ldkv + ks * 32 + g * 8) : zero8();
-  }
+  // ---- stage K, V, Q with coalesced loads (indices past the end are clamped:
+  // such keys are masked out below, such query rows are never stored)
   {
-    const int row = q0 + r;
+    bf16x8 kv[16], vv[16], qv[2];
+    // issue order = order of use: Q, K, then V (loads return in order)
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-      qf[ks] = row < a.rows ? load8(a.q + (size_t)row * a.ldq + ks * 32 + g * 8) : zero8();
+    for (int j = 0; j < 2; ++j) {
+      const int idx = t + 256 * j, row = idx >> 5, ch = idx & 31;
+      qv[j] = load8(a.q + (size_t)min(q0 + row, a.rows - 1) * a.ldq + ch * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int idx = t + 256 * j, key = idx >> 5, ch = idx & 31;
+      kv[j] = load8(a.k + (size_t)min(k0 + key, a.keys - 1) * a.ldkv + ch * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int idx = t + 256 * j, key = idx >> 5, ch = idx & 31;
+      vv[j] = load8(a.v + (size_t)min(k0 + key, a.keys - 1) * a.ldkv + ch * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int idx = t + 256 * j, key = idx >> 5, ch = idx & 31;
+      *reinterpret_cast<bf16x8*>(&ks_[key][ch * 8]) = kv[j];
+      *reinterpret_cast<bf16x8*>(&vs_[key][ch * 8]) = vv[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int idx = t + 256 * j, row = idx >> 5, ch = idx & 31;
+      *reinterpret_cast<bf16x8*>(&qs_[row][ch * 8]) = qv[j];
+    }
   }
+  __syncthreads();
 
-  // ---- S^T tiles: lane holds query row q0+r, keys kw0 + nt*16 + 4g + i
+  // ---- S^T tiles of this wave: lane holds query row q0+r, keys kw + nt*16 + 4g + i
+  const int kw = wave * 32;
   f32x4 st[2] = {zero4(), zero4()};
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
-    st[0] = mfma16(kf[0][ks], qf[ks], st[0]);
-    st[1] = mfma16(kf[1][ks], qf[ks], st[1]);
-  }
-
-  // ---- V -> LDS, transposed (vt[wave][d][key])
-#pragma unroll
-  for (int p = 0; p < 16; ++p) {
-    const int kk = lane & 31;
-    const int d = (p * 2 + (lane >> 5)) * 8;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) vt[wave][d + j][kk] = vreg[p][j];
+    const bf16x8 qf = *reinterpret_cast<const bf16x8*>(&qs_[r][ks * 32 + g * 8]);
+    const bf16x8 k0f = *reinterpret_cast<const bf16x8*>(&ks_[kw + r][ks * 32 + g * 8]);
+    const bf16x8 k1f = *reinterpret_cast<const bf16x8*>(&ks_[kw + 16 + r][ks * 32 + g * 8]);
+    st[0] = mfma16(k0f, qf, st[0]);
+    st[1] = mfma16(k1f, qf, st[1]);
   }
 
   // ---- masked log2-domain softmax of this wave's 32 keys
-  const int qrow = q0 + r;
-  const bool state_row = qrow < a.heads;
+  const bool state_row = q0 + r < a.heads;
   float s[8];
   float mx = NEG_BIG;
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int key = kw0 + nt * 16 + g * 4 + i;
+      const int key = k0 + kw + nt * 16 + g * 4 + i;
       const bool keep = key < a.keys && (!state_row || key <= a.enc_len);
       const float v = keep ? st[nt][i] * a.scale_log2 : NEG_BIG;
       s[nt * 4 + i] = v;
@@ -120,20 +128,23 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
   lsum += __shfl_xor(lsum, 16, PI0_WAVE);
   lsum += __shfl_xor(lsum, 32, PI0_WAVE);
   if (g == 0) { sm[wave][r] = mx; sl[wave][r] = lsum; }
-  __syncthreads();
 
-  // ---- O_w = P V_w : lane holds column dt*16 + r, query rows 4g + i
+  // ---- O_w = P V_w : B fragment = V[keys kw + {4g..4g+3, 16+4g..16+4g+3}][column]
   f32x4 o[16];
 #pragma unroll
   for (int dt = 0; dt < 16; ++dt) {
-    const __bf16* vp = &vt[wave][dt * 16 + r][0];
-    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vp + g * 4);
-    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vp + 16 + g * 4);
-    const bf16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    const int col = dt * 16 + r;
+    bf16x8 vf;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      vf[j] = vs_[kw + g * 4 + j][col];
+      vf[4 + j] = vs_[kw + 16 + g * 4 + j][col];
+    }
     o[dt] = mfma16(pf, vf, zero4());
   }
+  __syncthreads();          // sm/sl complete; every wave is done reading ks_
 
-  // ---- merge the 4 waves: O = sum_w 2^(m_w - M) O_w, L = sum_w 2^(m_w - M) l_w
+  // ---- merge the 4 waves: O = sum_w 2^(m_w - M) O_w (rows 4g+i of this lane)
   float alpha[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -144,82 +155,95 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
     const float mw = sm[wave][qr];
     alpha[i] = (mw <= 0.5f * NEG_BIG) ? 0.f : fast_exp2(mw - M);
   }
-  __syncthreads();                                   // all waves done reading vt
-  float* ob = reinterpret_cast<float*>(&vt[0][0][0]);   // [4][16][256] fp32 = 64 KB
+  float* ob = reinterpret_cast<float*>(&ks_[0][0]);      // [4][16][OBP] fp32
 #pragma unroll
   for (int dt = 0; dt < 16; ++dt)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      ob[(wave * ATT_QT + g * 4 + i) * ATT_HD + dt * 16 + r] = o[dt][i] * alpha[i];
+      ob[(wave * ATT_QT + g * 4 + i) * OBP + dt * 16 + r] = o[dt][i] * alpha[i];
   __syncthreads();
 
-  // thread t: query row t/16, columns 16*(t%16) .. +15
-  const int orow = t >> 4, oc = (t & 15) * 16;
-  float M = NEG_BIG;
+  // thread t owns 4 16-byte pieces: piece id = t + 256 j -> row id/64, columns 4*(id%64)..
+  f32x4 acc[4];
+  float rowM[4], rowL[4];
 #pragma unroll
-  for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w][orow]);
-  float L = 0.f;
+  for (int j = 0; j < 4; ++j) {
+    const int id = t + 256 * j, row = id >> 6, col = (id & 63) * 4;
+    float M = NEG_BIG;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    const float mw = sm[w][orow];
-    if (mw > 0.5f * NEG_BIG) L += fast_exp2(mw - M) * sl[w][orow];
-  }
-  const float inv = L > 0.f ? 1.0f / L : 0.f;
-  float acc[16];
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w][row]);
+    float L = 0.f;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    float v = 0.f;
+    for (int w = 0; w < 4; ++w) {
+      const float mw = sm[w][row];
+      if (mw > 0.5f * NEG_BIG) L += fast_exp2(mw - M) * sl[w][row];
+    }
+    f32x4 v = zero4();
 #pragma unroll
-    for (int w = 0; w < 4; ++w) v += ob[(w * ATT_QT + orow) * ATT_HD + oc + j];
+    for (int w = 0; w < 4; ++w) v += *reinterpret_cast<const f32x4*>(&ob[(w * ATT_QT + row) * OBP + col]);
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
     acc[j] = v * inv;
+    rowM[j] = M;
+    rowL[j] = L;
   }
-  const int grow = q0 + orow;
 
   if (a.nchunks == 1) {
-    if (grow < a.rows) {
-      bf16x8 lo, hi;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) { lo[j] = f2bf(acc[j]); hi[j] = f2bf(acc[8 + j]); }
-      *reinterpret_cast<bf16x8*>(a.out + (size_t)grow * a.ldo + oc) = lo;
-      *reinterpret_cast<bf16x8*>(a.out + (size_t)grow * a.ldo + oc + 8) = hi;
+    for (int j = 0; j < 4; ++j) {
+      const int id = t + 256 * j, grow = q0 + (id >> 6), col = (id & 63) * 4;
+      if (grow < a.rows) {
+        const bf16x4 pk = {f2bf(acc[j][0]), f2bf(acc[j][1]), f2bf(acc[j][2]), f2bf(acc[j][3])};
+        *reinterpret_cast<bf16x4*>(a.out + (size_t)grow * a.ldo + col) = pk;
+      }
     }
     return;
   }
 
-  // ---- several chunks: publish this chunk's partial, last arrival merges
-  {
-    float* pp = a.part + ((size_t)c * a.rows_pad + grow) * ATT_HD + oc;
+  // ---- several chunks: publish this chunk's partial, the last arrival merges
+  const __amdgpu_buffer_rsrc_t rp = dev_rsrc(a.part);
+  const __amdgpu_buffer_rsrc_t rl = dev_rsrc(a.lse);
 #pragma unroll
-    for (int j = 0; j < 16; j += 4) store_dev4(pp + j, f32x4{acc[j], acc[j + 1], acc[j + 2], acc[j + 3]});
-    if ((t & 15) == 0)
-      store_dev1(a.lse + (size_t)c * a.rows_pad + grow,
-                 (L > 0.f) ? M + log2f(L) : NEG_BIG);
+  for (int j = 0; j < 4; ++j) {
+    const int id = t + 256 * j, prow = q0 + (id >> 6), col = (id & 63) * 4;
+    dev_store4(rp, (int)(((size_t)c * a.rows_pad + prow) * ATT_HD + col) * 4, acc[j]);
+    if ((id & 63) == 0)
+      dev_store1(rl, (int)((size_t)c * a.rows_pad + prow) * 4,
+                 rowL[j] > 0.f ? rowM[j] + log2f(rowL[j]) : NEG_BIG);
   }
   if (!arrive_last(a.counters + qt, a.nchunks, &s_last)) return;
 
-  float lmax = NEG_BIG;
-  for (int cc = 0; cc < a.nchunks; ++cc) lmax = fmaxf(lmax, load_dev1(a.lse + (size_t)cc * a.rows_pad + grow));
-  float wsum = 0.f;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) acc[j] = 0.f;
-  for (int cc = 0; cc < a.nchunks; ++cc) {
-    const float l = load_dev1(a.lse + (size_t)cc * a.rows_pad + grow);
-    const float w = (l <= 0.5f * NEG_BIG) ? 0.f : fast_exp2(l - lmax);
-    wsum += w;
-    const float* pp = a.part + ((size_t)cc * a.rows_pad + grow) * ATT_HD + oc;
+  for (int j = 0; j < 4; ++j) {
+    const int id = t + 256 * j, prow = q0 + (id >> 6), col = (id & 63) * 4;
+    float lse_c[MAX_CHUNKS];
+    f32x4 pv[MAX_CHUNKS];
 #pragma unroll
-    for (int j = 0; j < 16; j += 4) {
-      const f32x4 pv = load_dev4(pp + j);
-      acc[j] += w * pv[0]; acc[j + 1] += w * pv[1]; acc[j + 2] += w * pv[2]; acc[j + 3] += w * pv[3];
+    for (int cc = 0; cc < MAX_CHUNKS; ++cc) {        // unconditional loads, clamped chunk
+      const int ci = min(cc, a.nchunks - 1);
+      lse_c[cc] = dev_load1(rl, (int)((size_t)ci * a.rows_pad + prow) * 4);
+      pv[cc] = dev_load4(rp, (int)(((size_t)ci * a.rows_pad + prow) * ATT_HD + col) * 4);
     }
-  }
-  if (grow < a.rows) {
-    const float winv = wsum > 0.f ? 1.0f / wsum : 0.f;
-    bf16x8 lo, hi;
+    float lmax = NEG_BIG;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) { lo[j] = f2bf(acc[j] * winv); hi[j] = f2bf(acc[8 + j] * winv); }
-    *reinterpret_cast<bf16x8*>(a.out + (size_t)grow * a.ldo + oc) = lo;
-    *reinterpret_cast<bf16x8*>(a.out + (size_t)grow * a.ldo + oc + 8) = hi;
+    for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
+      if (cc >= a.nchunks) lse_c[cc] = NEG_BIG;
+      lmax = fmaxf(lmax, lse_c[cc]);
+    }
+    float wsum = 0.f;
+    f32x4 o4 = zero4();
+#pragma unroll
+    for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
+      const float l = lse_c[cc];
+      const float w = (l <= 0.5f * NEG_BIG) ? 0.f : fast_exp2(l - lmax);
+      wsum += w;
+      o4 += w * pv[cc];
+    }
+    if (prow < a.rows) {
+      const float winv = wsum > 0.f ? 1.0f / wsum : 0.f;
+      const bf16x4 pk = {f2bf(o4[0] * winv), f2bf(o4[1] * winv), f2bf(o4[2] * winv),
+                         f2bf(o4[3] * winv)};
+      *reinterpret_cast<bf16x4*>(a.out + (size_t)prow * a.ldo + col) = pk;
+    }
   }
 }
 
@@ -244,7 +268,7 @@ int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int l
                      int ldo, int rows, int keys, int enc_len, int heads, int head_dim,
                      void* ws, size_t ws_bytes, hipStream_t s) {
   if (!q || !k || !v || !out || rows <= 0 || keys <= 0) return PI0HIP_ERR_ARG;
-  if (head_dim != ATT_HD) return PI0HIP_ERR_SHAPE;
+  if (head_dim != ATT_HD || keys > MAX_CHUNKS * ATT_CH) return PI0HIP_ERR_SHAPE;
   if (!ws || ws_bytes < pi0hip_attention_workspace_bytes(rows, keys)) return PI0HIP_ERR_WORKSPACE;
   AttnArgs a = {};
   a.q = (const __bf16*)q; a.ldq = ldq;

@@ -56,22 +56,24 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v));
 // On gfx950 every XCD has its own L2, and plain stores/loads are not coherent
 // across XCDs inside a kernel. Agent-scope fences (an L2 writeback or
 // invalidate) cost microseconds, so cross-workgroup data instead travels with
-// device-scope (sc1) stores and loads, which go to the memory-side coherence
+// device-scope (sc1) buffer loads/stores, which go to the memory-side coherence
 // point, and the producer waits for its stores to complete before it signals.
-__device__ __forceinline__ void store_dev4(float* p, f32x4 v) {
-  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+// Offsets are in bytes from the base of the buffer (< 2 GiB).
+constexpr int CPOL_SC1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
 }
-__device__ __forceinline__ void store_dev1(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void dev_store4(__amdgpu_buffer_rsrc_t r, int off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, CPOL_SC1);
 }
-__device__ __forceinline__ float load_dev1(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ f32x4 dev_load4(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CPOL_SC1));
 }
-// Four device-scope dword loads the compiler can keep in flight together.
-__device__ __forceinline__ f32x4 load_dev4(const float* p) {
-  f32x4 v;
-  v[0] = load_dev1(p); v[1] = load_dev1(p + 1); v[2] = load_dev1(p + 2); v[3] = load_dev1(p + 3);
-  return v;
+__device__ __forceinline__ void dev_store1(__amdgpu_buffer_rsrc_t r, int off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, CPOL_SC1);
+}
+__device__ __forceinline__ float dev_load1(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CPOL_SC1));
 }
 // Wait until every vector memory operation of this wave has completed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }

@@ -23,6 +23,8 @@
 
 namespace pi0 {
 
+constexpr int MAX_SPLITK = 8;
+
 enum Epi { EPI_BIAS = 0, EPI_RES = 1, EPI_RMS_BIAS_RES = 2, EPI_QKV_ROPE = 3, EPI_GATE = 4 };
 
 struct GemmArgs {
@@ -51,8 +53,12 @@ template <int EPI, bool DUAL, int KTW>
 __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   constexpr int ND = DUAL ? 2 : 1;
   constexpr bool RMS = uses_rms(EPI);
-  __shared__ float red[ND][4][4][4][PI0_WAVE];   // [acc][wave][mt][i][lane]
-  __shared__ float ssred[4][4][PI0_WAVE];        // [wave][mt][lane]
+  constexpr int KW = KTW * 32;            // k columns per wave
+  constexpr int XP = KW + 8;              // bf16 pitch of a staged x row (16 B pad: conflict-free reads)
+  constexpr int CHUNKS = KW / 8;          // 16-byte chunks per staged row
+  constexpr size_t X_BYTES = 4 * 64 * XP * 2;
+  constexpr size_t R_BYTES = (ND * 4 * 4 * 4 * PI0_WAVE + 4 * 4 * PI0_WAVE) * 4;
+  __shared__ __attribute__((aligned(16))) char smem[X_BYTES > R_BYTES ? X_BYTES : R_BYTES];
   __shared__ int s_last;
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -60,45 +66,72 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   const int nt = blockIdx.x / splitk, ks = blockIdx.x - nt * splitk;
   const int ntiles = a.N >> 4;
   const int mb = blockIdx.y, m0 = mb * 64;
+  const int rows = min(64, a.M - m0);
   const int KT = a.K >> 5;
   const int kt0 = ks * (KT / splitk) + wave * KTW;
 
-  // ---- weight stream: all fragments of this wave in flight together
+  // ---- stage this wave's x slice [rows x KW] in LDS with coalesced 16-byte loads.
+  // Chunk indices past the last row re-load the last chunk (unconditional loads,
+  // all in flight); LDS rows >= `rows` are never written and only reach output
+  // rows that are never stored.
+  __bf16* xs = reinterpret_cast<__bf16*>(smem) + wave * 64 * XP;
   bf16x8 b0[KTW], b1[KTW];
   {
-    const __bf16* wp = a.w0 + ((size_t)nt * KT + kt0) * 512 + lane * 8;
+    const int total = rows * CHUNKS;
+    bf16x8 xv[(64 * CHUNKS) / PI0_WAVE];
 #pragma unroll
-    for (int i = 0; i < KTW; ++i) b0[i] = load8(wp + i * 512);
-    if constexpr (DUAL) {
-      const __bf16* wq = a.w1 + ((size_t)nt * KT + kt0) * 512 + lane * 8;
+    for (int it = 0; it < (64 * CHUNKS) / PI0_WAVE; ++it) {
+      const int idx = min(it * PI0_WAVE + lane, total - 1);
+      const int row = idx / CHUNKS, ch = idx - row * CHUNKS;
+      xv[it] = load8(a.x + (size_t)(m0 + row) * a.ldx + kt0 * 32 + ch * 8);
+    }
+    // weight stream, issued after the (L2-resident) x loads: loads return in
+    // order, so x is usable as soon as it lands and each MFMA waits only for
+    // the weight fragments it consumes. All fragments of the wave in flight.
+    {
+      const __bf16* wp = a.w0 + ((size_t)nt * KT + kt0) * 512 + lane * 8;
 #pragma unroll
-      for (int i = 0; i < KTW; ++i) b1[i] = load8(wq + i * 512);
+      for (int i = 0; i < KTW; ++i) b0[i] = load8(wp + i * 512);
+      if constexpr (DUAL) {
+        const __bf16* wq = a.w1 + ((size_t)nt * KT + kt0) * 512 + lane * 8;
+#pragma unroll
+        for (int i = 0; i < KTW; ++i) b1[i] = load8(wq + i * 512);
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < (64 * CHUNKS) / PI0_WAVE; ++it) {
+      const int idx = min(it * PI0_WAVE + lane, total - 1);
+      const int row = idx / CHUNKS, ch = idx - row * CHUNKS;
+      *reinterpret_cast<bf16x8*>(xs + row * XP + ch * 8) = xv[it];
     }
   }
-  // ---- activation fragments (rows past M read as zero)
-  const int r = lane & 15, g = lane >> 4;
-  bf16x8 av[4][KTW];
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    const int row = m0 + mt * 16 + r;
-    const __bf16* xp = a.x + (size_t)row * a.ldx + kt0 * 32 + g * 8;
-#pragma unroll
-    for (int i = 0; i < KTW; ++i) av[mt][i] = row < a.M ? load8(xp + i * 32) : zero8();
-  }
+  // (each wave reads only the rows it staged itself: no workgroup barrier needed)
 
+  const int r = lane & 15, g = lane >> 4;
   f32x4 acc0[4], acc1[4];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) { acc0[mt] = zero4(); acc1[mt] = zero4(); }
+  float ssl[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < KTW; ++i) {
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-      acc0[mt] = mfma16(av[mt][i], b0[i], acc0[mt]);
-      if constexpr (DUAL) acc1[mt] = mfma16(av[mt][i], b1[i], acc1[mt]);
+      const bf16x8 av = *reinterpret_cast<const bf16x8*>(xs + (mt * 16 + r) * XP + i * 32 + g * 8);
+      acc0[mt] = mfma16(av, b0[i], acc0[mt]);
+      if constexpr (DUAL) acc1[mt] = mfma16(av, b1[i], acc1[mt]);
+      if constexpr (RMS) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) { const float v = bf2f(av[j]); ssl[mt] += v * v; }
+      }
     }
   }
+  __syncthreads();                        // x staging area becomes the reduction area
 
   // ---- intra-workgroup reduction over the 4 waves' K ranges
+  typedef float RedT[4][4][4][PI0_WAVE];  // [wave][mt][i][lane]
+  RedT* red = reinterpret_cast<RedT*>(smem);
+  float (*ssred)[4][PI0_WAVE] = reinterpret_cast<float (*)[4][PI0_WAVE]>(
+      smem + ND * sizeof(RedT));
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
@@ -106,18 +139,7 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
       red[0][wave][mt][i][lane] = acc0[mt][i];
       if constexpr (DUAL) red[ND - 1][wave][mt][i][lane] = acc1[mt][i];
     }
-  }
-  if constexpr (RMS) {
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      float s = 0.f;
-#pragma unroll
-      for (int i = 0; i < KTW; ++i) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) { float v = bf2f(av[mt][i][j]); s += v * v; }
-      }
-      ssred[wave][mt][lane] = s;
-    }
+    if constexpr (RMS) ssred[wave][mt][lane] = ssl[mt];
   }
   __syncthreads();
 
@@ -146,29 +168,42 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   if (splitk > 1) {
     const int tile = mb * ntiles + nt;
     const size_t tiles = (size_t)gridDim.y * ntiles;
-    float* part = a.ws;
-    float* ssp = a.ws + part_floats((int)tiles, splitk, ND);
+    // partial tile layout: [tile][split][64 rows][16 * ND] fp32, then [tile][split][64] sums
+    const __amdgpu_buffer_rsrc_t rs = dev_rsrc(a.ws);
+    const int ss_base = (int)(part_floats((int)tiles, splitk, ND) * 4);
     {
-      float* p = part + (((size_t)tile * splitk + ks) * 64 + lrow) * 16 * ND + c4;
-      store_dev4(p, f32x4{v0[0], v0[1], v0[2], v0[3]});
-      if constexpr (DUAL) store_dev4(p + 16, f32x4{v1[0], v1[1], v1[2], v1[3]});
-      if (RMS && (t & 3) == 0) store_dev1(ssp + ((size_t)tile * splitk + ks) * 64 + lrow, ss);
+      const int off = (int)((((size_t)tile * splitk + ks) * 64 + lrow) * 16 * ND + c4) * 4;
+      dev_store4(rs, off, f32x4{v0[0], v0[1], v0[2], v0[3]});
+      if constexpr (DUAL) dev_store4(rs, off + 64, f32x4{v1[0], v1[1], v1[2], v1[3]});
+      if (RMS && (t & 3) == 0)
+        dev_store1(rs, ss_base + (int)(((size_t)tile * splitk + ks) * 64 + lrow) * 4, ss);
     }
     if (!arrive_last(a.counters + tile, splitk, &s_last)) return;
+    // all partial loads in flight together (splitk <= MAX_SPLITK), summed in split order
+    f32x4 q0[MAX_SPLITK], q1[MAX_SPLITK];
+    float qs[MAX_SPLITK];
+#pragma unroll
+    for (int k = 0; k < MAX_SPLITK; ++k) {
+      const int kk = min(k, splitk - 1);     // unconditional loads; extra ones are ignored
+      const int off = (int)((((size_t)tile * splitk + kk) * 64 + lrow) * 16 * ND + c4) * 4;
+      q0[k] = dev_load4(rs, off);
+      if constexpr (DUAL) q1[k] = dev_load4(rs, off + 64);
+      if constexpr (RMS) qs[k] = dev_load1(rs, ss_base + (int)(((size_t)tile * splitk + kk) * 64 + lrow) * 4);
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) { v0[c] = 0.f; v1[c] = 0.f; }
     ss = 0.f;
-    for (int k = 0; k < splitk; ++k) {
-      const float* p = part + (((size_t)tile * splitk + k) * 64 + lrow) * 16 * ND + c4;
-      const f32x4 q0 = load_dev4(p);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) v0[c] += q0[c];
-      if constexpr (DUAL) {
-        const f32x4 q1 = load_dev4(p + 16);
+    for (int k = 0; k < MAX_SPLITK; ++k) {
+      if (k < splitk) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) v1[c] += q1[c];
+        for (int c = 0; c < 4; ++c) v0[c] += q0[k][c];
+        if constexpr (DUAL) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c) v1[c] += q1[k][c];
+        }
+        if constexpr (RMS) ss += qs[k];
       }
-      if constexpr (RMS) ss += load_dev1(ssp + ((size_t)tile * splitk + k) * 64 + lrow);
     }
   }
 
@@ -225,7 +260,7 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
 template <int EPI, bool DUAL>
 static int launch_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0 || a.K <= 0) return PI0HIP_ERR_ARG;
-  if (a.K % 32 || a.N % 16 || a.splitk < 1) return PI0HIP_ERR_SHAPE;
+  if (a.K % 32 || a.N % 16 || a.splitk < 1 || a.splitk > MAX_SPLITK) return PI0HIP_ERR_SHAPE;
   const int KT = a.K / 32;
   if (KT % (4 * a.splitk)) return PI0HIP_ERR_SHAPE;
   if (a.splitk > 1 && (!a.ws || !a.counters)) return PI0HIP_ERR_WORKSPACE;

@@ -88,7 +88,7 @@ size_t pi0hip_attention_workspace_bytes(int rows, int keys);
 
 /* out = softmax(mask(q k^T / sqrt(head_dim))) v over `keys` cache rows; flat
  * query row r = token * heads + head; rows r < heads keep keys j <= enc_len.
- * `out` may alias `q`. head_dim must be 256.
+ * `out` may alias `q`. head_dim must be 256, keys <= 1024.
  * decoder_attention fused_wrappers.py:88-115 (tl_fd_flat_split + tl_fd_flat_combine,
  * kernels/base.py:801-923) */
 int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int ldkv, void* out,
