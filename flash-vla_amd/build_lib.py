@@ -8,6 +8,7 @@ from __future__ import annotations
 import concurrent.futures as cf
 import glob
 import os
+import re
 import subprocess
 import sys
 
@@ -38,12 +39,28 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
+# packed fp32 VALU forms must not appear in the device code (see FLAGS)
+_PACKED_FP32 = re.compile(r"\bv_pk_(add|mul|fma)_f32\b")
+
+
+def check_no_packed_fp32(src: str) -> None:
+    """Compile `src` to device assembly and fail if any packed fp32 VALU op was generated."""
+    cmd = [HIPCC, *FLAGS, "--cuda-device-only", "-S", src, "-o", "-"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed for {src}:\n{res.stderr}")
+    if _PACKED_FP32.search(res.stdout):
+        raise RuntimeError(f"{src}: packed fp32 VALU instructions in the device code")
+
+
+def build(verbose: bool = False, check_isa: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
         objs = list(ex.map(_compile, sources))
+        if check_isa:
+            list(ex.map(check_no_packed_fp32, sources))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)

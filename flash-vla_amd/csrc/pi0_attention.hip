@@ -37,7 +37,8 @@ struct AttnArgs {
   const __bf16* k; const __bf16* v; int ldkv;
   __bf16* out; int ldo;
   float* part; float* lse; int* counters;
-  int rows, keys, enc_len, heads, nchunks, rows_pad;
+  int rows, keys, enc_len, heads, nchunks, rows_pad, nqt;
+  int xcd_local;    // chunks of one query tile share an XCD: merge through its L2
   float scale_log2;
 };
 
@@ -50,9 +51,22 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int qt = blockIdx.x, c = blockIdx.y;
+  // 1-D grid. XCD-local mode: ids congruent mod 8 share an XCD, so the chunks of
+  // query tile qt all run on XCD qt % 8 (tile ids padded to a multiple of 8).
+  const bool local = a.xcd_local != 0;
+  int qt, c;
+  if (local) {
+    const int x = blockIdx.x & (NUM_XCD - 1), j = blockIdx.x / NUM_XCD;
+    c = j % a.nchunks;
+    qt = (j / a.nchunks) * NUM_XCD + x;
+  } else {
+    qt = blockIdx.x % a.nqt;
+    c = blockIdx.x / a.nqt;
+  }
+  if (qt >= a.nqt) return;          // padding workgroup (no barrier or counter touched)
   const int q0 = qt * ATT_QT, k0 = c * ATT_CH;
 
+  PI0_PROBE(0);
   // ---- stage K, V, Q with coalesced loads (indices past the end are clamped:
   // such keys are masked out below, such query rows are never stored)
   {
@@ -86,6 +100,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
     }
   }
   __syncthreads();
+  PI0_PROBE(1);
 
   // ---- S^T tiles of this wave: lane holds query row q0+r, keys kw + nt*16 + 4g + i
   const int kw = wave * 32;
@@ -129,6 +144,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
   lsum += __shfl_xor(lsum, 32, PI0_WAVE);
   if (g == 0) { sm[wave][r] = mx; sl[wave][r] = lsum; }
 
+  PI0_PROBE(2);
   // ---- O_w = P V_w : B fragment = V[keys kw + {4g..4g+3, 16+4g..16+4g+3}][column]
   f32x4 o[16];
 #pragma unroll
@@ -142,6 +158,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
     }
     o[dt] = mfma16(pf, vf, zero4());
   }
+  PI0_PROBE(3);
   __syncthreads();          // sm/sl complete; every wave is done reading ks_
 
   // ---- merge the 4 waves: O = sum_w 2^(m_w - M) O_w (rows 4g+i of this lane)
@@ -152,8 +169,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
     float M = NEG_BIG;
 #pragma unroll
     for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w][qr]);
-    const float mw = sm[wave][qr];
-    alpha[i] = (mw <= 0.5f * NEG_BIG) ? 0.f : fast_exp2(mw - M);
+    alpha[i] = fast_exp2(sm[wave][qr] - M);   // 0 for an empty wave next to a non-empty one
   }
   float* ob = reinterpret_cast<float*>(&ks_[0][0]);      // [4][16][OBP] fp32
 #pragma unroll
@@ -163,6 +179,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
       ob[(wave * ATT_QT + g * 4 + i) * OBP + dt * 16 + r] = o[dt][i] * alpha[i];
   __syncthreads();
 
+  PI0_PROBE(4);
   // thread t owns 4 16-byte pieces: piece id = t + 256 j -> row id/64, columns 4*(id%64)..
   f32x4 acc[4];
   float rowM[4], rowL[4];
@@ -172,16 +189,14 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
     float M = NEG_BIG;
 #pragma unroll
     for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w][row]);
+    // branch-free: an empty wave has m_w = NEG_BIG and l_w = 0, so its term is 0
     float L = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float mw = sm[w][row];
-      if (mw > 0.5f * NEG_BIG) L += fast_exp2(mw - M) * sl[w][row];
-    }
+    for (int w = 0; w < 4; ++w) L += fast_exp2(sm[w][row] - M) * sl[w][row];
     f32x4 v = zero4();
 #pragma unroll
     for (int w = 0; w < 4; ++w) v += *reinterpret_cast<const f32x4*>(&ob[(w * ATT_QT + row) * OBP + col]);
-    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    const float inv = L > 0.f ? __builtin_amdgcn_rcpf(L) : 0.f;
     acc[j] = v * inv;
     rowM[j] = M;
     rowL[j] = L;
@@ -205,12 +220,15 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int id = t + 256 * j, prow = q0 + (id >> 6), col = (id & 63) * 4;
-    dev_store4(rp, (int)(((size_t)c * a.rows_pad + prow) * ATT_HD + col) * 4, acc[j]);
+    part_store4(a.part, rp, (int)(((size_t)c * a.rows_pad + prow) * ATT_HD + col) * 4, acc[j],
+                local);
     if ((id & 63) == 0)
-      dev_store1(rl, (int)((size_t)c * a.rows_pad + prow) * 4,
-                 rowL[j] > 0.f ? rowM[j] + log2f(rowL[j]) : NEG_BIG);
+      part_store1(a.lse, rl, (int)((size_t)c * a.rows_pad + prow) * 4,
+                  rowL[j] > 0.f ? rowM[j] + __builtin_amdgcn_logf(rowL[j]) : NEG_BIG, local);
   }
-  if (!arrive_last(a.counters + qt, a.nchunks, &s_last)) return;
+  PI0_PROBE(5);
+  if (!arrive_last(a.counters + qt, a.nchunks, &s_last, local)) return;
+  PI0_PROBE(6);
 
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -220,26 +238,28 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int cc = 0; cc < MAX_CHUNKS; ++cc) {        // unconditional loads, clamped chunk
       const int ci = min(cc, a.nchunks - 1);
-      lse_c[cc] = dev_load1(rl, (int)((size_t)ci * a.rows_pad + prow) * 4);
-      pv[cc] = dev_load4(rp, (int)(((size_t)ci * a.rows_pad + prow) * ATT_HD + col) * 4);
+      lse_c[cc] = part_load1(a.lse, rl, (int)((size_t)ci * a.rows_pad + prow) * 4, local);
+      pv[cc] = part_load4(a.part, rp, (int)(((size_t)ci * a.rows_pad + prow) * ATT_HD + col) * 4,
+                          local);
     }
     float lmax = NEG_BIG;
 #pragma unroll
     for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
-      if (cc >= a.nchunks) lse_c[cc] = NEG_BIG;
+      lse_c[cc] = cc < a.nchunks ? lse_c[cc] : NEG_BIG;
       lmax = fmaxf(lmax, lse_c[cc]);
     }
+    // chunks past the end and empty chunks carry NEG_BIG: weight 2^(NEG_BIG - lmax) = 0
+    // (when every chunk is empty all partials are 0 and so is the result)
     float wsum = 0.f;
     f32x4 o4 = zero4();
 #pragma unroll
     for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
-      const float l = lse_c[cc];
-      const float w = (l <= 0.5f * NEG_BIG) ? 0.f : fast_exp2(l - lmax);
+      const float w = cc < a.nchunks ? fast_exp2(lse_c[cc] - lmax) : 0.f;
       wsum += w;
       o4 += w * pv[cc];
     }
     if (prow < a.rows) {
-      const float winv = wsum > 0.f ? 1.0f / wsum : 0.f;
+      const float winv = wsum > 0.f ? __builtin_amdgcn_rcpf(wsum) : 0.f;
       const bf16x4 pk = {f2bf(o4[0] * winv), f2bf(o4[1] * winv), f2bf(o4[2] * winv),
                          f2bf(o4[3] * winv)};
       *reinterpret_cast<bf16x4*>(a.out + (size_t)prow * a.ldo + col) = pk;
@@ -278,6 +298,9 @@ int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int l
   a.nchunks = (keys + ATT_CH - 1) / ATT_CH;
   const int nqt = (rows + ATT_QT - 1) / ATT_QT;
   a.rows_pad = nqt * ATT_QT;
+  a.nqt = nqt;
+  a.xcd_local = (a.nchunks > 1 && pi0hip_xcd_dispatch_ok()) ? 1 : 0;
+  const int grid = (a.xcd_local ? (nqt + NUM_XCD - 1) / NUM_XCD * NUM_XCD : nqt) * a.nchunks;
   char* base = reinterpret_cast<char*>(ws);
   a.counters = reinterpret_cast<int*>(base);
   base += round256((size_t)nqt * sizeof(int));
@@ -285,7 +308,7 @@ int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int l
   base += round256((size_t)a.nchunks * a.rows_pad * sizeof(float));
   a.part = reinterpret_cast<float*>(base);
   a.scale_log2 = 1.4426950408889634f / sqrtf((float)head_dim);
-  hipLaunchKernelGGL(attn_kernel, dim3(nqt, a.nchunks), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(attn_kernel, dim3(grid), dim3(256), 0, s, a);
   return (int)hipGetLastError();
 }
 

@@ -37,6 +37,7 @@ struct GemmArgs {
   __bf16* norm_factor;
   float* ws; int* counters;
   int M, N, K, splitk, heads, head_dim;
+  int xcd_local;   // split-K partners share an XCD: exchange partials through its L2
 };
 
 constexpr bool uses_rms(int epi) {
@@ -63,8 +64,17 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int splitk = a.splitk;
-  const int nt = blockIdx.x / splitk, ks = blockIdx.x - nt * splitk;
   const int ntiles = a.N >> 4;
+  const bool local = a.xcd_local != 0;
+  int nt, ks;
+  if (local) {   // ids congruent mod 8 share an XCD: the splits of one tile all do
+    const int x = blockIdx.x & (NUM_XCD - 1), j = blockIdx.x / NUM_XCD;
+    ks = j % splitk;
+    nt = (j / splitk) * NUM_XCD + x;
+  } else {
+    nt = blockIdx.x / splitk;
+    ks = blockIdx.x - nt * splitk;
+  }
   const int mb = blockIdx.y, m0 = mb * 64;
   const int rows = min(64, a.M - m0);
   const int KT = a.K >> 5;
@@ -173,12 +183,12 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
     const int ss_base = (int)(part_floats((int)tiles, splitk, ND) * 4);
     {
       const int off = (int)((((size_t)tile * splitk + ks) * 64 + lrow) * 16 * ND + c4) * 4;
-      dev_store4(rs, off, f32x4{v0[0], v0[1], v0[2], v0[3]});
-      if constexpr (DUAL) dev_store4(rs, off + 64, f32x4{v1[0], v1[1], v1[2], v1[3]});
+      part_store4(a.ws, rs, off, f32x4{v0[0], v0[1], v0[2], v0[3]}, local);
+      if constexpr (DUAL) part_store4(a.ws, rs, off + 64, f32x4{v1[0], v1[1], v1[2], v1[3]}, local);
       if (RMS && (t & 3) == 0)
-        dev_store1(rs, ss_base + (int)(((size_t)tile * splitk + ks) * 64 + lrow) * 4, ss);
+        part_store1(a.ws, rs, ss_base + (int)(((size_t)tile * splitk + ks) * 64 + lrow) * 4, ss, local);
     }
-    if (!arrive_last(a.counters + tile, splitk, &s_last)) return;
+    if (!arrive_last(a.counters + tile, splitk, &s_last, local)) return;
     // all partial loads in flight together (splitk <= MAX_SPLITK), summed in split order
     f32x4 q0[MAX_SPLITK], q1[MAX_SPLITK];
     float qs[MAX_SPLITK];
@@ -186,9 +196,9 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
     for (int k = 0; k < MAX_SPLITK; ++k) {
       const int kk = min(k, splitk - 1);     // unconditional loads; extra ones are ignored
       const int off = (int)((((size_t)tile * splitk + kk) * 64 + lrow) * 16 * ND + c4) * 4;
-      q0[k] = dev_load4(rs, off);
-      if constexpr (DUAL) q1[k] = dev_load4(rs, off + 64);
-      if constexpr (RMS) qs[k] = dev_load1(rs, ss_base + (int)(((size_t)tile * splitk + kk) * 64 + lrow) * 4);
+      q0[k] = part_load4(a.ws, rs, off, local);
+      if constexpr (DUAL) q1[k] = part_load4(a.ws, rs, off + 64, local);
+      if constexpr (RMS) qs[k] = part_load1(a.ws, rs, ss_base + (int)(((size_t)tile * splitk + kk) * 64 + lrow) * 4, local);
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) { v0[c] = 0.f; v1[c] = 0.f; }
@@ -265,12 +275,14 @@ static int launch_gemm(const GemmArgs& a, hipStream_t s) {
   if (KT % (4 * a.splitk)) return PI0HIP_ERR_SHAPE;
   if (a.splitk > 1 && (!a.ws || !a.counters)) return PI0HIP_ERR_WORKSPACE;
   const int ktw = KT / (4 * a.splitk);
+  GemmArgs b = a;
+  b.xcd_local = (a.splitk > 1 && (a.N / 16) % NUM_XCD == 0 && pi0hip_xcd_dispatch_ok()) ? 1 : 0;
   dim3 grid((a.N / 16) * a.splitk, (a.M + 63) / 64);
   switch (ktw) {
-    case 1: skinny_gemm_kernel<EPI, DUAL, 1><<<grid, 256, 0, s>>>(a); break;
-    case 2: skinny_gemm_kernel<EPI, DUAL, 2><<<grid, 256, 0, s>>>(a); break;
-    case 4: skinny_gemm_kernel<EPI, DUAL, 4><<<grid, 256, 0, s>>>(a); break;
-    case 8: skinny_gemm_kernel<EPI, DUAL, 8><<<grid, 256, 0, s>>>(a); break;
+    case 1: skinny_gemm_kernel<EPI, DUAL, 1><<<grid, 256, 0, s>>>(b); break;
+    case 2: skinny_gemm_kernel<EPI, DUAL, 2><<<grid, 256, 0, s>>>(b); break;
+    case 4: skinny_gemm_kernel<EPI, DUAL, 4><<<grid, 256, 0, s>>>(b); break;
+    case 8: skinny_gemm_kernel<EPI, DUAL, 8><<<grid, 256, 0, s>>>(b); break;
     default: return PI0HIP_ERR_SHAPE;
   }
   return (int)hipGetLastError();

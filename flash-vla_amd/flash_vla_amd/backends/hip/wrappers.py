@@ -44,6 +44,8 @@ def scratch(role: str, shape, dtype, device) -> torch.Tensor:
 
 
 def _stream() -> int:
+    if not _capturing():
+        _abi.ensure_init()
     return torch.cuda.current_stream().cuda_stream
 
 

@@ -29,8 +29,25 @@ extern "C" {
 #define PI0HIP_ERR_SHAPE (-2)      /* shape the kernels do not support         */
 #define PI0HIP_ERR_WORKSPACE (-3)  /* workspace missing or too small           */
 
-/* Library version: 100 * major + minor. */
+/* Library version. */
 int pi0hip_version(void);
+
+/* One-time set-up for the current device (call once per device, outside graph
+ * capture; allocates a few KB and synchronises). It verifies that workgroups
+ * are dispatched round-robin over the 8 XCDs, which lets split-K and attention
+ * partials of one tile travel through a single XCD's L2. Without it (or with
+ * PI0HIP_XCD_LOCAL=0 in the environment) the kernels use device-scope traffic
+ * instead; results are the same either way. No reference counterpart. */
+int pi0hip_init(void);
+
+/* 1 if pi0hip_init verified the XCD dispatch order on the current device
+ * (and the XCD-local exchange is switched on). */
+int pi0hip_xcd_dispatch_ok(void);
+
+/* Switch the XCD-local exchange off (0) or back on (1, only after pi0hip_init
+ * verified the dispatch order) for the current device; a diagnostic and test
+ * hook that selects between two paths with identical results. */
+int pi0hip_set_xcd_local(int enable);
 
 /* W[batch][K][N] -> B-fragment packed copy of the same size. K % 32 == 0, N % 16 == 0.
  * Replaces nothing in the reference (TileLang reads the [K, N] weights through

@@ -178,3 +178,30 @@ def test_layer_views_of_a_stacked_weight():
         W.decoder_out_proj_residual(x.to(DEV), ws[i], out)
         close(out, O.op_matmul_residual(x.float(), ws[i].cpu().float(), torch.zeros(51, 1024)),
               what=f"layer {i}")
+
+
+def test_xcd_local_exchange_matches_device_scope_path():
+    """Split-K and attention partials merged through one XCD's L2 or through device-scope
+    traffic: same summation order, so results must be identical bit for bit."""
+    from flash_vla_amd.backends.hip import _abi
+    lib = _abi.lib()
+    _abi.ensure_init()
+    print(f"\nXCD round-robin dispatch verified: {lib.pi0hip_xcd_dispatch_ok()}")
+    x, w, r = rnd((51, 4096), 40).to(DEV), rnd((4096, 1024), 41, 0.02).to(DEV), rnd((51, 1024), 42)
+    q, k, v = rnd((408, 256), 43).to(DEV), rnd((819, 256), 44).to(DEV), rnd((819, 256), 45).to(DEV)
+    outs = []
+    try:
+        for enable in (0, 1):
+            if enable and not lib.pi0hip_xcd_dispatch_ok() and lib.pi0hip_set_xcd_local(1) != 0:
+                pytest.skip("XCD dispatch order not verified on this device")
+            _abi.check(lib.pi0hip_set_xcd_local(enable), "pi0hip_set_xcd_local")
+            out = r.to(DEV)
+            W.decoder_ffn_down_residual(x, w, out)
+            Q = q.clone()
+            W.decoder_attention(Q, k, v, None, Q, 768)
+            torch.cuda.synchronize()
+            outs.append((out.cpu(), Q.cpu()))
+    finally:
+        lib.pi0hip_set_xcd_local(1)
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1])
