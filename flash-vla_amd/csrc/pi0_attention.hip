@@ -38,7 +38,6 @@ struct AttnArgs {
   __bf16* out; int ldo;
   float* part; float* lse; int* counters;
   int rows, keys, enc_len, heads, nchunks, rows_pad, nqt;
-  int xcd_local;    // chunks of one query tile share an XCD: merge through its L2
   float scale_log2;
 };
 
@@ -51,19 +50,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int r = lane & 15, g = lane >> 4;
-  // 1-D grid. XCD-local mode: ids congruent mod 8 share an XCD, so the chunks of
-  // query tile qt all run on XCD qt % 8 (tile ids padded to a multiple of 8).
-  const bool local = a.xcd_local != 0;
-  int qt, c;
-  if (local) {
-    const int x = blockIdx.x & (NUM_XCD - 1), j = blockIdx.x / NUM_XCD;
-    c = j % a.nchunks;
-    qt = (j / a.nchunks) * NUM_XCD + x;
-  } else {
-    qt = blockIdx.x % a.nqt;
-    c = blockIdx.x / a.nqt;
-  }
-  if (qt >= a.nqt) return;          // padding workgroup (no barrier or counter touched)
+  const int qt = blockIdx.x % a.nqt, c = blockIdx.x / a.nqt;
   const int q0 = qt * ATT_QT, k0 = c * ATT_CH;
 
   PI0_PROBE(0);
@@ -220,14 +207,13 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int id = t + 256 * j, prow = q0 + (id >> 6), col = (id & 63) * 4;
-    part_store4(a.part, rp, (int)(((size_t)c * a.rows_pad + prow) * ATT_HD + col) * 4, acc[j],
-                local);
+    dev_store4(rp, (int)(((size_t)c * a.rows_pad + prow) * ATT_HD + col) * 4, acc[j]);
     if ((id & 63) == 0)
-      part_store1(a.lse, rl, (int)((size_t)c * a.rows_pad + prow) * 4,
-                  rowL[j] > 0.f ? rowM[j] + __builtin_amdgcn_logf(rowL[j]) : NEG_BIG, local);
+      dev_store1(rl, (int)((size_t)c * a.rows_pad + prow) * 4,
+                 rowL[j] > 0.f ? rowM[j] + __builtin_amdgcn_logf(rowL[j]) : NEG_BIG);
   }
   PI0_PROBE(5);
-  if (!arrive_last(a.counters + qt, a.nchunks, &s_last, local)) return;
+  if (!arrive_last(a.counters + qt, a.nchunks, &s_last)) return;
   PI0_PROBE(6);
 
 #pragma unroll
@@ -238,9 +224,8 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int cc = 0; cc < MAX_CHUNKS; ++cc) {        // unconditional loads, clamped chunk
       const int ci = min(cc, a.nchunks - 1);
-      lse_c[cc] = part_load1(a.lse, rl, (int)((size_t)ci * a.rows_pad + prow) * 4, local);
-      pv[cc] = part_load4(a.part, rp, (int)(((size_t)ci * a.rows_pad + prow) * ATT_HD + col) * 4,
-                          local);
+      lse_c[cc] = dev_load1(rl, (int)((size_t)ci * a.rows_pad + prow) * 4);
+      pv[cc] = dev_load4(rp, (int)(((size_t)ci * a.rows_pad + prow) * ATT_HD + col) * 4);
     }
     float lmax = NEG_BIG;
 #pragma unroll
@@ -299,8 +284,7 @@ int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int l
   const int nqt = (rows + ATT_QT - 1) / ATT_QT;
   a.rows_pad = nqt * ATT_QT;
   a.nqt = nqt;
-  a.xcd_local = (a.nchunks > 1 && pi0hip_xcd_dispatch_ok()) ? 1 : 0;
-  const int grid = (a.xcd_local ? (nqt + NUM_XCD - 1) / NUM_XCD * NUM_XCD : nqt) * a.nchunks;
+  const int grid = nqt * a.nchunks;
   char* base = reinterpret_cast<char*>(ws);
   a.counters = reinterpret_cast<int*>(base);
   base += round256((size_t)nqt * sizeof(int));

@@ -81,55 +81,19 @@ __device__ __forceinline__ void dev_store1(__amdgpu_buffer_rsrc_t r, int off, fl
 __device__ __forceinline__ float dev_load1(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CPOL_SC1));
 }
-// ---- exchange inside one XCD ---------------------------------------------------
-// Workgroups whose linear ids are congruent modulo 8 are dispatched to the same
-// XCD (round-robin dispatch; verified once per device by pi0hip_init). Stores
-// are written through the CU's L1 into that XCD's L2, so a consumer on the same
-// XCD sees them with plain loads once its own L1 is invalidated.
-constexpr int NUM_XCD = 8;
-__device__ __forceinline__ int xcd_id() { return __builtin_amdgcn_s_getreg(0xF814) & 0xF; }
-__device__ __forceinline__ void invalidate_l1() { asm volatile("buffer_inv sc0" ::: "memory"); }
-
-// Partial-result exchange: XCD-local (plain stores, L1-invalidated plain loads)
-// when `local`, device-scope sc1 traffic otherwise.
-__device__ __forceinline__ void part_store4(float* base, __amdgpu_buffer_rsrc_t r, int off, f32x4 v,
-                                            bool local) {
-  if (local) *reinterpret_cast<f32x4*>(reinterpret_cast<char*>(base) + off) = v;
-  else dev_store4(r, off, v);
-}
-__device__ __forceinline__ f32x4 part_load4(const float* base, __amdgpu_buffer_rsrc_t r, int off,
-                                            bool local) {
-  return local ? *reinterpret_cast<const f32x4*>(reinterpret_cast<const char*>(base) + off)
-               : dev_load4(r, off);
-}
-__device__ __forceinline__ void part_store1(float* base, __amdgpu_buffer_rsrc_t r, int off, float v,
-                                            bool local) {
-  if (local) *reinterpret_cast<float*>(reinterpret_cast<char*>(base) + off) = v;
-  else dev_store1(r, off, v);
-}
-__device__ __forceinline__ float part_load1(const float* base, __amdgpu_buffer_rsrc_t r, int off,
-                                            bool local) {
-  return local ? *reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + off)
-               : dev_load1(r, off);
-}
-
 // Wait until every vector memory operation of this wave has completed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Arrival counter for "last workgroup finishes": every thread has issued its
 // device-scope stores; returns true (in all threads) for the last of `total`
 // arrivals, which also resets the counter for the next launch.
-// With `local` (all arrivals on this XCD) the last workgroup invalidates its L1
-// so that its plain loads see the other workgroups' partials in the shared L2.
-__device__ __forceinline__ bool arrive_last(int* counter, int total, int* s_flag,
-                                            bool local = false) {
+__device__ __forceinline__ bool arrive_last(int* counter, int total, int* s_flag) {
   wait_vmem();
   __syncthreads();
   if (threadIdx.x == 0) {
     const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int last = prev == total - 1;
     if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (last && local) invalidate_l1();
     *s_flag = last;
   }
   __syncthreads();

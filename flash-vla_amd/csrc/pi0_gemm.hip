@@ -37,7 +37,7 @@ struct GemmArgs {
   __bf16* norm_factor;
   float* ws; int* counters;
   int M, N, K, splitk, heads, head_dim;
-  int xcd_local;   // split-K partners share an XCD: exchange partials through its L2
+  float* out_f32;  // EPI_RMS_BIAS_RES: fp32 residual / destination instead of `out`
 };
 
 constexpr bool uses_rms(int epi) {
@@ -65,16 +65,7 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int splitk = a.splitk;
   const int ntiles = a.N >> 4;
-  const bool local = a.xcd_local != 0;
-  int nt, ks;
-  if (local) {   // ids congruent mod 8 share an XCD: the splits of one tile all do
-    const int x = blockIdx.x & (NUM_XCD - 1), j = blockIdx.x / NUM_XCD;
-    ks = j % splitk;
-    nt = (j / splitk) * NUM_XCD + x;
-  } else {
-    nt = blockIdx.x / splitk;
-    ks = blockIdx.x - nt * splitk;
-  }
+  const int nt = blockIdx.x / splitk, ks = blockIdx.x - nt * splitk;
   const int mb = blockIdx.y, m0 = mb * 64;
   const int rows = min(64, a.M - m0);
   const int KT = a.K >> 5;
@@ -183,12 +174,12 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
     const int ss_base = (int)(part_floats((int)tiles, splitk, ND) * 4);
     {
       const int off = (int)((((size_t)tile * splitk + ks) * 64 + lrow) * 16 * ND + c4) * 4;
-      part_store4(a.ws, rs, off, f32x4{v0[0], v0[1], v0[2], v0[3]}, local);
-      if constexpr (DUAL) part_store4(a.ws, rs, off + 64, f32x4{v1[0], v1[1], v1[2], v1[3]}, local);
+      dev_store4(rs, off, f32x4{v0[0], v0[1], v0[2], v0[3]});
+      if constexpr (DUAL) dev_store4(rs, off + 64, f32x4{v1[0], v1[1], v1[2], v1[3]});
       if (RMS && (t & 3) == 0)
-        part_store1(a.ws, rs, ss_base + (int)(((size_t)tile * splitk + ks) * 64 + lrow) * 4, ss, local);
+        dev_store1(rs, ss_base + (int)(((size_t)tile * splitk + ks) * 64 + lrow) * 4, ss);
     }
-    if (!arrive_last(a.counters + tile, splitk, &s_last, local)) return;
+    if (!arrive_last(a.counters + tile, splitk, &s_last)) return;
     // all partial loads in flight together (splitk <= MAX_SPLITK), summed in split order
     f32x4 q0[MAX_SPLITK], q1[MAX_SPLITK];
     float qs[MAX_SPLITK];
@@ -196,9 +187,9 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
     for (int k = 0; k < MAX_SPLITK; ++k) {
       const int kk = min(k, splitk - 1);     // unconditional loads; extra ones are ignored
       const int off = (int)((((size_t)tile * splitk + kk) * 64 + lrow) * 16 * ND + c4) * 4;
-      q0[k] = part_load4(a.ws, rs, off, local);
-      if constexpr (DUAL) q1[k] = part_load4(a.ws, rs, off + 64, local);
-      if constexpr (RMS) qs[k] = part_load1(a.ws, rs, ss_base + (int)(((size_t)tile * splitk + kk) * 64 + lrow) * 4, local);
+      q0[k] = dev_load4(rs, off);
+      if constexpr (DUAL) q1[k] = dev_load4(rs, off + 64);
+      if constexpr (RMS) qs[k] = dev_load1(rs, ss_base + (int)(((size_t)tile * splitk + kk) * 64 + lrow) * 4);
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) { v0[c] = 0.f; v1[c] = 0.f; }
@@ -233,6 +224,15 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) o[c] = v0[c] + bf2f(rp[c]);
   } else if constexpr (EPI == EPI_RMS_BIAS_RES) {
+    if (a.out_f32) {            // fp32 Euler accumulator: read, update and store in fp32
+      float* rp = a.out_f32 + (size_t)row * a.ldo + n;
+      const f32x4 r4 = *reinterpret_cast<const f32x4*>(rp);
+      f32x4 o4;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o4[c] = v0[c] * f + bf2f(a.bias[n + c]) + r4[c];
+      *reinterpret_cast<f32x4*>(rp) = o4;
+      return;
+    }
     const __bf16* rp = a.out + (size_t)row * a.ldo + n;
 #pragma unroll
     for (int c = 0; c < 4; ++c) o[c] = v0[c] * f + bf2f(a.bias[n + c]) + bf2f(rp[c]);
@@ -275,14 +275,12 @@ static int launch_gemm(const GemmArgs& a, hipStream_t s) {
   if (KT % (4 * a.splitk)) return PI0HIP_ERR_SHAPE;
   if (a.splitk > 1 && (!a.ws || !a.counters)) return PI0HIP_ERR_WORKSPACE;
   const int ktw = KT / (4 * a.splitk);
-  GemmArgs b = a;
-  b.xcd_local = (a.splitk > 1 && (a.N / 16) % NUM_XCD == 0 && pi0hip_xcd_dispatch_ok()) ? 1 : 0;
   dim3 grid((a.N / 16) * a.splitk, (a.M + 63) / 64);
   switch (ktw) {
-    case 1: skinny_gemm_kernel<EPI, DUAL, 1><<<grid, 256, 0, s>>>(b); break;
-    case 2: skinny_gemm_kernel<EPI, DUAL, 2><<<grid, 256, 0, s>>>(b); break;
-    case 4: skinny_gemm_kernel<EPI, DUAL, 4><<<grid, 256, 0, s>>>(b); break;
-    case 8: skinny_gemm_kernel<EPI, DUAL, 8><<<grid, 256, 0, s>>>(b); break;
+    case 1: skinny_gemm_kernel<EPI, DUAL, 1><<<grid, 256, 0, s>>>(a); break;
+    case 2: skinny_gemm_kernel<EPI, DUAL, 2><<<grid, 256, 0, s>>>(a); break;
+    case 4: skinny_gemm_kernel<EPI, DUAL, 4><<<grid, 256, 0, s>>>(a); break;
+    case 8: skinny_gemm_kernel<EPI, DUAL, 8><<<grid, 256, 0, s>>>(a); break;
     default: return PI0HIP_ERR_SHAPE;
   }
   return (int)hipGetLastError();
@@ -380,6 +378,18 @@ int pi0hip_rms_linear_bias_residual(const void* x, int ldx, const void* wp, cons
   if (!x || !wp || !bias || !out) return PI0HIP_ERR_ARG;
   GemmArgs a = base_args(x, ldx, wp, out, ldo, M, N, K, splitk);
   a.bias = (const __bf16*)bias;
+  if (int e = setup_ws(a, ws, ws_bytes, 0)) return e;
+  return launch_gemm<EPI_RMS_BIAS_RES, false>(a, s);
+}
+
+int pi0hip_rms_linear_bias_residual_f32(const void* x, int ldx, const void* wp, const void* bias,
+                                        float* out, int ldo, int M, int N, int K, int splitk,
+                                        void* ws, size_t ws_bytes, hipStream_t s) {
+  if (!x || !wp || !bias || !out) return PI0HIP_ERR_ARG;
+  if (ldo % 4) return PI0HIP_ERR_SHAPE;
+  GemmArgs a = base_args(x, ldx, wp, nullptr, ldo, M, N, K, splitk);
+  a.bias = (const __bf16*)bias;
+  a.out_f32 = out;
   if (int e = setup_ws(a, ws, ws_bytes, 0)) return e;
   return launch_gemm<EPI_RMS_BIAS_RES, false>(a, s);
 }

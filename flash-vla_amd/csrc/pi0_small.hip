@@ -8,9 +8,9 @@
 
 namespace pi0 {
 
-template <int K>
+template <int K, typename XT>
 __global__ __launch_bounds__(256) void small_k_linear_kernel(
-    const __bf16* __restrict__ x, int ldx, const __bf16* __restrict__ w,
+    const XT* __restrict__ x, int ldx, const __bf16* __restrict__ w,
     const __bf16* __restrict__ bias, __bf16* __restrict__ out, int ldo, int M, int N, int act) {
   const int groups = N / 8;
   const int id = blockIdx.x * blockDim.x + threadIdx.x;
@@ -21,7 +21,7 @@ __global__ __launch_bounds__(256) void small_k_linear_kernel(
   for (int k = 0; k < K; ++k) wv[k] = load8(w + (size_t)k * N + n);
   float xv[K];
 #pragma unroll
-  for (int k = 0; k < K; ++k) xv[k] = bf2f(x[(size_t)m * ldx + k]);
+  for (int k = 0; k < K; ++k) xv[k] = static_cast<float>(x[(size_t)m * ldx + k]);
   const bf16x8 bv = load8(bias + n);
   bf16x8 o;
 #pragma unroll
@@ -38,15 +38,27 @@ __global__ __launch_bounds__(256) void small_k_linear_kernel(
 
 }  // namespace pi0
 
-extern "C" int pi0hip_small_linear(const void* x, int ldx, const void* w, const void* bias,
-                                   void* out, int ldo, int M, int N, int K, int act,
-                                   hipStream_t s) {
+template <typename XT>
+static int launch_small(const void* x, int ldx, const void* w, const void* bias, void* out, int ldo,
+                        int M, int N, int K, int act, hipStream_t s) {
   if (!x || !w || !bias || !out || M <= 0 || N <= 0 || K <= 0) return PI0HIP_ERR_ARG;
   if (act != 0 && act != 1) return PI0HIP_ERR_ARG;
   if (N % 8 || K != 32 || ldo % 8) return PI0HIP_ERR_SHAPE;
   const int threads = M * (N / 8);
-  hipLaunchKernelGGL(pi0::small_k_linear_kernel<32>, dim3((threads + 255) / 256), dim3(256), 0, s,
-                     (const __bf16*)x, ldx, (const __bf16*)w, (const __bf16*)bias, (__bf16*)out,
+  hipLaunchKernelGGL((pi0::small_k_linear_kernel<32, XT>), dim3((threads + 255) / 256), dim3(256),
+                     0, s, (const XT*)x, ldx, (const __bf16*)w, (const __bf16*)bias, (__bf16*)out,
                      ldo, M, N, act);
   return (int)hipGetLastError();
+}
+
+extern "C" int pi0hip_small_linear(const void* x, int ldx, const void* w, const void* bias,
+                                   void* out, int ldo, int M, int N, int K, int act,
+                                   hipStream_t s) {
+  return launch_small<__bf16>(x, ldx, w, bias, out, ldo, M, N, K, act, s);
+}
+
+extern "C" int pi0hip_small_linear_f32x(const void* x, int ldx, const void* w, const void* bias,
+                                        void* out, int ldo, int M, int N, int K, int act,
+                                        hipStream_t s) {
+  return launch_small<float>(x, ldx, w, bias, out, ldo, M, N, K, act, s);
 }

@@ -17,12 +17,12 @@ P = c_void_p
 # name -> (restype, argtypes); must match include/pi0_hip.h exactly.
 PROTOTYPES = {
     "pi0hip_version": (c_int, []),
-    "pi0hip_init": (c_int, []),
-    "pi0hip_xcd_dispatch_ok": (c_int, []),
-    "pi0hip_set_xcd_local": (c_int, [c_int]),
     "pi0hip_pack_weight": (c_int, [P, P, c_int, c_int, c_int, P]),
     "pi0hip_gemm_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
     "pi0hip_small_linear": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),
+    "pi0hip_small_linear_f32x": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, c_int, P]),
+    "pi0hip_rms_linear_bias_residual_f32": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int,
+                                                    c_int, P, c_size_t, P]),
     "pi0hip_linear_bias": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, c_int,
                                    P, c_size_t, P]),
     "pi0hip_linear_residual": (c_int, [P, c_int, P, P, c_int, c_int, c_int, c_int, c_int,
@@ -64,19 +64,6 @@ def lib() -> ctypes.CDLL:
             fn.argtypes = args
         _lib = handle
     return _lib
-
-
-_INITIALISED: set = set()
-
-
-def ensure_init() -> None:
-    """Run pi0hip_init once per device (needs a GPU; never during graph capture)."""
-    import torch
-
-    dev = torch.cuda.current_device()
-    if dev not in _INITIALISED:
-        check(lib().pi0hip_init(), "pi0hip_init")
-        _INITIALISED.add(dev)
 
 
 def check(rc: int, name: str) -> None:

@@ -44,8 +44,6 @@ def scratch(role: str, shape, dtype, device) -> torch.Tensor:
 
 
 def _stream() -> int:
-    if not _capturing():
-        _abi.ensure_init()
     return torch.cuda.current_stream().cuda_stream
 
 
@@ -53,8 +51,8 @@ def _capturing() -> bool:
     return torch.cuda.is_current_stream_capturing()
 
 
-def _check(t: torch.Tensor, name: str, ndim: int | None = None) -> None:
-    if t.dtype != torch.bfloat16:
+def _check(t: torch.Tensor, name: str, ndim: int | None = None, allow_f32: bool = False) -> None:
+    if t.dtype != torch.bfloat16 and not (allow_f32 and t.dtype == torch.float32):
         raise TypeError(f"{name}: expected bfloat16, got {t.dtype}")
     if not t.is_cuda:
         raise ValueError(f"{name}: expected a GPU tensor")
@@ -163,14 +161,16 @@ def decoder_state_proj(x, weight, bias, out):
 
 
 def decoder_action_in_proj(x, weight, bias, out):
-    """out = silu(x @ weight + bias) (wrappers.py:115-120)."""
-    _check(x, "x", 2); _check(weight, "weight", 2); _check(bias, "bias", 1); _check(out, "out", 2)
+    """out = silu(x @ weight + bias) (wrappers.py:115-120); x may be the fp32 noise accumulator."""
+    _check(x, "x", 2, allow_f32=True); _check(weight, "weight", 2); _check(bias, "bias", 1)
+    _check(out, "out", 2)
     M, K = x.shape
     N = weight.shape[1]
     if weight.shape[0] != K or out.shape != (M, N) or bias.shape != (N,):
         raise ValueError("decoder_action_in_proj: shape mismatch")
-    _abi.call("pi0hip_small_linear", _ptr(x), x.stride(0), _ptr(weight), _ptr(bias), _ptr(out),
-              out.stride(0), M, N, K, 1, _stream())
+    fn = "pi0hip_small_linear_f32x" if x.dtype == torch.float32 else "pi0hip_small_linear"
+    _abi.call(fn, _ptr(x), x.stride(0), _ptr(weight), _ptr(bias), _ptr(out), out.stride(0),
+              M, N, K, 1, _stream())
     return out
 
 
@@ -272,7 +272,7 @@ def decoder_norm_gated_ffn(x, gate_w, up_w, out, norm_factor):
 
 
 def _action_out(x, weight, bias, out):
-    _check(x, "x", 2); _check(bias, "bias", 1); _check(out, "out", 2)
+    _check(x, "x", 2); _check(bias, "bias", 1); _check(out, "out", 2, allow_f32=True)
     M, K = x.shape
     N = weight.shape[1]
     if weight.shape[0] != K or out.shape != (M, N) or bias.shape != (N,):
@@ -280,8 +280,10 @@ def _action_out(x, weight, bias, out):
     wp = packed_weight_ptr(weight)
     s = _splitk(M, N, K)
     ws, nbytes = _gemm_ws("gemm_ws_out", M, N, s, 0, x.device)
-    _abi.call("pi0hip_rms_linear_bias_residual", _ptr(x), x.stride(0), wp, _ptr(bias), _ptr(out),
-              out.stride(0), M, N, K, s, ws, nbytes, _stream())
+    fn = ("pi0hip_rms_linear_bias_residual_f32" if out.dtype == torch.float32
+          else "pi0hip_rms_linear_bias_residual")
+    _abi.call(fn, _ptr(x), x.stride(0), wp, _ptr(bias), _ptr(out), out.stride(0), M, N, K, s, ws,
+              nbytes, _stream())
     return out
 
 

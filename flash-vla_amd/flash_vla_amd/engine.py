@@ -30,7 +30,7 @@ class Pi0DecoderEngine:
     def __init__(self, weights: dict, encoder_seq_len: int = 768, chunk_size: int = 50,
                  steps: int = 10, layers: int = 18, fused: bool = True, backend: str = "hip",
                  plan: dict | None = None, device: str = "cuda", capture: bool = True,
-                 warmup: int = 3):
+                 warmup: int = 3, fp32_euler: bool = True):
         self.encoder_seq_len = encoder_seq_len
         self.chunk_size = chunk_size
         self.steps = steps
@@ -53,6 +53,10 @@ class Pi0DecoderEngine:
             encoder_seq_len, chunk_size, device, layers=n_layers, width=dims["width"],
             ffn=dims["ffn"], heads=dims["heads"], head_dim=dims["head_dim"],
             action_dim=dims["action_dim"])
+        if fp32_euler:
+            # the Euler accumulator stays fp32 between steps; diffusion_noise (bf16) is the output
+            self.buffers["diffusion_noise_f32"] = torch.zeros(
+                chunk_size, dims["action_dim"], dtype=torch.float32, device=device)
         self.pool = ScratchPool()
         self.graph = None
         if hasattr(self.backend, "prepare_weights"):
@@ -68,6 +72,7 @@ class Pi0DecoderEngine:
 
     def _capture(self, warmup: int):
         saved = self.buffers["diffusion_noise"].clone()
+        self._sync_master()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
@@ -81,6 +86,11 @@ class Pi0DecoderEngine:
             self._run()
         torch.cuda.synchronize()
         self.buffers["diffusion_noise"].copy_(saved)
+        self._sync_master()
+
+    def _sync_master(self):
+        if "diffusion_noise_f32" in self.buffers:
+            self.buffers["diffusion_noise_f32"].copy_(self.buffers["diffusion_noise"])
 
     def load_prefix(self, prefix_k: torch.Tensor, prefix_v: torch.Tensor) -> None:
         """Copy the prefix K/V ([layers, >= enc_len, head_dim]) into the static cache."""
@@ -92,6 +102,8 @@ class Pi0DecoderEngine:
         """Denoise one action chunk; returns the static `diffusion_noise` buffer."""
         self.buffers["observation_state_normalized"].copy_(state)
         self.buffers["diffusion_noise"].copy_(noise)
+        if "diffusion_noise_f32" in self.buffers:
+            self.buffers["diffusion_noise_f32"].copy_(noise)
         if self.graph is not None:
             self.graph.replay()
         else:
@@ -99,6 +111,7 @@ class Pi0DecoderEngine:
         return self.buffers["diffusion_noise"]
 
     def replay(self) -> None:
+        """Replay the captured loop on whatever the static buffers hold (benchmarks)."""
         self.graph.replay()
 
 

@@ -4,6 +4,11 @@ Pure orchestration: every line is an op-table call on static buffers, so the
 loop captures into one hipGraph. Sequence = one state token + the action
 chunk; each Euler step re-projects the noise, runs the layers against the
 prefix KV cache and updates `diffusion_noise` in place.
+
+When the buffers also hold `diffusion_noise_f32`, that fp32 tensor is the Euler
+accumulator (read by the in-projection, updated by the out-projection) and is
+rounded into the bf16 `diffusion_noise` once, after the last step; otherwise
+the bf16 buffer itself is updated every step, as in the reference.
 """
 from __future__ import annotations
 
@@ -13,10 +18,11 @@ def transformer_decoder(ops, weights, buffers, encoder_seq_len, steps=10, layers
         buffers["observation_state_normalized"], weights["decoder_state_in_proj_w"],
         weights["decoder_state_in_proj_b"], buffers["decoder_state_buf"])
 
+    noise = buffers.get("diffusion_noise_f32", buffers["diffusion_noise"])
     for step in range(steps):
         buffers["decoder_x"][:1].copy_(buffers["decoder_state_buf"])
         ops.decoder_action_in_proj(
-            buffers["diffusion_noise"], weights["decoder_action_fused_in_proj_w"],
+            noise, weights["decoder_action_fused_in_proj_w"],
             weights["decoder_action_fused_time_biases"][step % 10], buffers["decoder_x_buf"])
         ops.decoder_action_mlp(
             buffers["decoder_x_buf"], weights["decoder_action_mlp_w"],
@@ -44,5 +50,8 @@ def transformer_decoder(ops, weights, buffers, encoder_seq_len, steps=10, layers
 
         ops.decoder_action_out_proj(
             buffers["decoder_x"][1:], weights["decoder_action_fused_out_proj_w"],
-            weights["decoder_action_fused_out_proj_b"], buffers["diffusion_noise"],
+            weights["decoder_action_fused_out_proj_b"], noise,
             buffers["decoder_norm_factor_buf"])
+
+    if noise is not buffers["diffusion_noise"]:
+        buffers["diffusion_noise"].copy_(noise)

@@ -32,23 +32,6 @@ extern "C" {
 /* Library version. */
 int pi0hip_version(void);
 
-/* One-time set-up for the current device (call once per device, outside graph
- * capture; allocates a few KB and synchronises). It verifies that workgroups
- * are dispatched round-robin over the 8 XCDs, which lets split-K and attention
- * partials of one tile travel through a single XCD's L2. Without it (or with
- * PI0HIP_XCD_LOCAL=0 in the environment) the kernels use device-scope traffic
- * instead; results are the same either way. No reference counterpart. */
-int pi0hip_init(void);
-
-/* 1 if pi0hip_init verified the XCD dispatch order on the current device
- * (and the XCD-local exchange is switched on). */
-int pi0hip_xcd_dispatch_ok(void);
-
-/* Switch the XCD-local exchange off (0) or back on (1, only after pi0hip_init
- * verified the dispatch order) for the current device; a diagnostic and test
- * hook that selects between two paths with identical results. */
-int pi0hip_set_xcd_local(int enable);
-
 /* W[batch][K][N] -> B-fragment packed copy of the same size. K % 32 == 0, N % 16 == 0.
  * Replaces nothing in the reference (TileLang reads the [K, N] weights through
  * TMA); this is the one-time relayout that makes the weight stream coalesced. */
@@ -64,6 +47,11 @@ size_t pi0hip_gemm_workspace_bytes(int M, int N, int splitk, int dual);
  * decoder_action_in_proj wrappers.py:115-120 (tl_matmul_bias_silu, kernels/base.py:304-335) */
 int pi0hip_small_linear(const void* x, int ldx, const void* w, const void* bias, void* out,
                         int ldo, int M, int N, int K, int act, hipStream_t s);
+
+/* pi0hip_small_linear with an fp32 x (the fp32 Euler accumulator as the
+ * action_in_proj input). Same reference call site. */
+int pi0hip_small_linear_f32x(const void* x, int ldx, const void* w, const void* bias, void* out,
+                             int ldo, int M, int N, int K, int act, hipStream_t s);
 
 /* out = x @ W + bias, fp32 accumulation, M <= 64 per 64-row block.
  * decoder_action_mlp wrappers.py:123-128 (tl_matmul_bias, kernels/base.py:158-192) */
@@ -84,6 +72,12 @@ int pi0hip_linear_residual(const void* x, int ldx, const void* w_packed, void* o
 int pi0hip_rms_linear_bias_residual(const void* x, int ldx, const void* w_packed,
                                     const void* bias, void* out, int ldo, int M, int N, int K,
                                     int splitk, void* ws, size_t ws_bytes, hipStream_t s);
+
+/* pi0hip_rms_linear_bias_residual with an fp32 residual / destination (the
+ * Euler accumulator kept in fp32 between steps; ldo % 4 == 0). Same call site. */
+int pi0hip_rms_linear_bias_residual_f32(const void* x, int ldx, const void* w_packed,
+                                        const void* bias, float* out, int ldo, int M, int N, int K,
+                                        int splitk, void* ws, size_t ws_bytes, hipStream_t s);
 
 /* acc = f * (x @ Wqkv), RoPE on adjacent pairs of the first (heads+1)*head_dim
  * columns with rope[m] = interleaved bf16 (cos, sin); scatter to

@@ -7,9 +7,10 @@ and noise [50, 32] N(0, 1), 10 Euler steps.
 Tolerances (written per test):
   * 1 step: every stored activation is rounded to bf16 at the same points in
     both, so noise agrees to max abs <= 2e-2, cosine >= 0.99999;
-  * 10 steps vs the fp32 oracle: the bf16 `diffusion_noise` buffer of the
-    reference's per-op contract is re-rounded every step (half an ulp is 0.0078
-    at |x| ~ 4), so the per-op loop is held to max abs <= 6e-2, cosine >= 0.9999.
+  * 10 steps vs the fp32 oracle with the Euler accumulator in fp32 (the
+    engine default): BASELINE's bound, max abs <= 2e-2 and cosine >= 0.999;
+  * 10 steps with the reference's bf16 `diffusion_noise` contract (re-rounded
+    every step; half an ulp is 0.0078 at |x| ~ 4): max abs <= 6e-2, cosine >= 0.9999.
 """
 import pytest
 import torch
@@ -41,10 +42,10 @@ def case():
     return ck, inp
 
 
-def _engine(case, steps, layers, capture=True):
+def _engine(case, steps, layers, capture=True, fp32_euler=True):
     ck, inp = case
     eng = Pi0DecoderEngine({k: v.to(DEV) for k, v in ck.items()}, steps=steps, layers=layers,
-                           capture=capture)
+                           capture=capture, fp32_euler=fp32_euler)
     eng.load_prefix(inp["encoder_K"].to(DEV), inp["encoder_V"].to(DEV))
     return eng
 
@@ -90,17 +91,22 @@ def test_one_step_full_depth(case):
     assert (1 - g_cos) <= 1.5 * (1 - e_cos) and g_err <= 1.5 * e_err
 
 
-def test_ten_steps_graph(case):
-    eng = _engine(case, 10, 18, capture=True)
+@pytest.mark.parametrize("fp32_euler", [True, False])
+def test_ten_steps_graph(case, fp32_euler):
+    eng = _engine(case, 10, 18, capture=True, fp32_euler=fp32_euler)
     state = case[1]["observation_state_normalized"].to(DEV)
     noise0 = case[1]["diffusion_noise"].to(DEV)
     out1 = eng.forward(state, noise0).clone()
     out2 = eng.forward(state, noise0).clone()
+    assert out1.dtype == torch.bfloat16
     assert torch.equal(out1, out2), "graph replays differ"
     ref, _, _, _ = _oracle(case, 10, 18, bf16=False)
     err, cos = _metrics(out1, ref)
-    print(f"\n10 steps x 18 layers (graph): max abs {err:.3e} cos {cos:.7f}")
-    assert err <= 6e-2 and cos >= 0.9999
+    print(f"\n10 steps x 18 layers (graph, fp32 Euler {fp32_euler}): max abs {err:.3e} cos {cos:.7f}")
+    if fp32_euler:
+        assert err <= 2e-2 and cos >= 0.999
+    else:
+        assert err <= 6e-2 and cos >= 0.9999
 
 
 def test_graph_equals_eager(case):

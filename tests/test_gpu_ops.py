@@ -75,6 +75,14 @@ def test_action_in_proj():
     close(out, O.op_action_in_proj(x.float(), w.float(), b.float()), what="action_in")
 
 
+def test_action_in_proj_fp32_input():
+    x = torch.randn(50, 32, generator=torch.Generator().manual_seed(36))
+    w, b = rnd((32, 1024), 37, 0.02), rnd(1024, 38, 0.5)
+    out = torch.zeros(50, 1024, dtype=torch.bfloat16, device=DEV)
+    W.decoder_action_in_proj(x.to(DEV), w.to(DEV), b.to(DEV), out)
+    close(out, O.op_action_in_proj(x, w.float(), b.float()), what="action_in fp32 x")
+
+
 def test_action_mlp_into_row_view():
     x, w, b = rnd((50, 1024), 8), rnd((1024, 1024), 9, 0.02), rnd(1024, 10, 0.02)
     xbuf = torch.full((51, 1024), 7.0, dtype=torch.bfloat16, device=DEV)
@@ -169,6 +177,20 @@ def test_action_out_proj_euler_update():
           what="out_proj")
 
 
+def test_action_out_proj_fp32_accumulator():
+    xfull = rnd((51, 1024), 46)
+    w, b = rnd((1024, 32), 47, 0.002), rnd(32, 48, 0.002)
+    noise = torch.randn(50, 32, generator=torch.Generator().manual_seed(49))
+    out = noise.to(DEV)
+    W.decoder_action_out_proj(xfull.to(DEV)[1:], w.to(DEV), b.to(DEV), out, None)
+    x = xfull[1:].float()
+    f = O.rms_factor(x, bf16=True)[:, None]          # the factor is rounded to bf16, as in the reference
+    ref = noise + b.float() + (x @ w.float()) * f    # everything else stays fp32
+    assert out.dtype == torch.float32
+    err = (out.cpu() - ref).abs().max().item()
+    assert err <= 1e-5, err          # only fp32 summation order differs
+
+
 def test_layer_views_of_a_stacked_weight():
     """Per-layer views of one [L, K, N] stack resolve to the right packed layer."""
     ws = rnd((3, 2048, 1024), 34, 0.02).to(DEV)
@@ -179,29 +201,3 @@ def test_layer_views_of_a_stacked_weight():
         close(out, O.op_matmul_residual(x.float(), ws[i].cpu().float(), torch.zeros(51, 1024)),
               what=f"layer {i}")
 
-
-def test_xcd_local_exchange_matches_device_scope_path():
-    """Split-K and attention partials merged through one XCD's L2 or through device-scope
-    traffic: same summation order, so results must be identical bit for bit."""
-    from flash_vla_amd.backends.hip import _abi
-    lib = _abi.lib()
-    _abi.ensure_init()
-    print(f"\nXCD round-robin dispatch verified: {lib.pi0hip_xcd_dispatch_ok()}")
-    x, w, r = rnd((51, 4096), 40).to(DEV), rnd((4096, 1024), 41, 0.02).to(DEV), rnd((51, 1024), 42)
-    q, k, v = rnd((408, 256), 43).to(DEV), rnd((819, 256), 44).to(DEV), rnd((819, 256), 45).to(DEV)
-    outs = []
-    try:
-        for enable in (0, 1):
-            if enable and not lib.pi0hip_xcd_dispatch_ok() and lib.pi0hip_set_xcd_local(1) != 0:
-                pytest.skip("XCD dispatch order not verified on this device")
-            _abi.check(lib.pi0hip_set_xcd_local(enable), "pi0hip_set_xcd_local")
-            out = r.to(DEV)
-            W.decoder_ffn_down_residual(x, w, out)
-            Q = q.clone()
-            W.decoder_attention(Q, k, v, None, Q, 768)
-            torch.cuda.synchronize()
-            outs.append((out.cpu(), Q.cpu()))
-    finally:
-        lib.pi0hip_set_xcd_local(1)
-    assert torch.equal(outs[0][0], outs[1][0])
-    assert torch.equal(outs[0][1], outs[1][1])
