@@ -58,46 +58,15 @@ __device__ __forceinline__ float gelu_tanh(float v) {
 }
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
 
-// ---- device-coherent exchange between workgroups of one launch ---------------
-// On gfx950 every XCD has its own L2, and plain stores/loads are not coherent
-// across XCDs inside a kernel. Agent-scope fences (an L2 writeback or
-// invalidate) cost microseconds, so cross-workgroup data instead travels with
-// device-scope (sc1) buffer loads/stores, which go to the memory-side coherence
-// point, and the producer waits for its stores to complete before it signals.
-// Offsets are in bytes from the base of the buffer (< 2 GiB).
-constexpr int CPOL_SC1 = 16;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+// ---- bounds-checked row loads ---------------------------------------------------
+// A buffer resource covering exactly `nbytes` makes every load past the end return
+// zeros without faulting, so staging loops need no clamping or branches and their
+// offsets stay 32-bit (row * pitch + column, plus per-iteration immediates).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nbytes, 0x00020000);
 }
-__device__ __forceinline__ void dev_store4(__amdgpu_buffer_rsrc_t r, int off, f32x4 v) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, CPOL_SC1);
-}
-__device__ __forceinline__ f32x4 dev_load4(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CPOL_SC1));
-}
-__device__ __forceinline__ void dev_store1(__amdgpu_buffer_rsrc_t r, int off, float v) {
-  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, CPOL_SC1);
-}
-__device__ __forceinline__ float dev_load1(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CPOL_SC1));
-}
-// Wait until every vector memory operation of this wave has completed.
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-// Arrival counter for "last workgroup finishes": every thread has issued its
-// device-scope stores; returns true (in all threads) for the last of `total`
-// arrivals, which also resets the counter for the next launch.
-__device__ __forceinline__ bool arrive_last(int* counter, int total, int* s_flag) {
-  wait_vmem();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = prev == total - 1;
-    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *s_flag = last;
-  }
-  __syncthreads();
-  return *s_flag != 0;
+__device__ __forceinline__ bf16x8 buf_load8(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
 __device__ __forceinline__ float warp_sum(float v) {

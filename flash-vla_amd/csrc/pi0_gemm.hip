@@ -35,7 +35,7 @@ struct GemmArgs {
   __bf16* out_k; __bf16* out_v; int ldkv;
   const __bf16* rope;
   __bf16* norm_factor;
-  float* ws; int* counters;
+  float* ws;
   int M, N, K, splitk, heads, head_dim;
   float* out_f32;  // EPI_RMS_BIAS_RES: fp32 residual / destination instead of `out`
 };
@@ -50,6 +50,71 @@ __host__ __device__ inline size_t part_floats(int tiles, int splitk, int nd) {
   return (size_t)tiles * splitk * 64 * 16 * nd;
 }
 
+// Epilogue of one 4-column piece of output row `row` (columns nt*16 + c4 ..+3) from
+// the fp32 accumulators v0 (and v1 for the dual gate/up GEMM) and, for the RMS
+// call sites, the row's sum of squares over the full K.
+template <int EPI, bool DUAL>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int row, int nt, int c4,
+                                              bool nf_writer, const float* v0, const float* v1,
+                                              float ss) {
+  constexpr bool RMS = uses_rms(EPI);
+  if (row >= a.M) return;
+  const int n = nt * 16 + c4;
+  float f = 1.f;
+  if constexpr (RMS) f = round_bf(rsqrtf(ss / (float)a.K + 1e-6f));
+
+  float o[4];
+  if constexpr (EPI == EPI_BIAS) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = v0[c] + bf2f(a.bias[n + c]);
+  } else if constexpr (EPI == EPI_RES) {
+    const __bf16* rp = a.out + (size_t)row * a.ldo + n;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = v0[c] + bf2f(rp[c]);
+  } else if constexpr (EPI == EPI_RMS_BIAS_RES) {
+    if (a.out_f32) {            // fp32 Euler accumulator: read, update and store in fp32
+      float* rp = a.out_f32 + (size_t)row * a.ldo + n;
+      const f32x4 r4 = *reinterpret_cast<const f32x4*>(rp);
+      f32x4 o4;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o4[c] = v0[c] * f + bf2f(a.bias[n + c]) + r4[c];
+      *reinterpret_cast<f32x4*>(rp) = o4;
+      return;
+    }
+    const __bf16* rp = a.out + (size_t)row * a.ldo + n;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = v0[c] * f + bf2f(a.bias[n + c]) + bf2f(rp[c]);
+  } else if constexpr (EPI == EPI_GATE) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = gelu_tanh(v0[c] * f) * (v1[c] * f);
+  } else if constexpr (EPI == EPI_QKV_ROPE) {
+    const int hd = a.head_dim, qdim = a.heads * hd;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = v0[c] * f;
+    if (n < qdim + hd) {
+      const int rj = n % hd;
+      const __bf16* rp = a.rope + (size_t)row * hd + rj;
+#pragma unroll
+      for (int p = 0; p < 4; p += 2) {
+        const float cs = bf2f(rp[p]), sn = bf2f(rp[p + 1]);
+        const float x0 = o[p], x1 = o[p + 1];
+        o[p] = x0 * cs - x1 * sn;
+        o[p + 1] = x1 * cs + x0 * sn;
+      }
+    }
+    __bf16* dst;
+    if (n < qdim) dst = a.out + (size_t)row * qdim + n;
+    else if (n < qdim + hd) dst = a.out_k + (size_t)row * a.ldkv + (n - qdim);
+    else dst = a.out_v + (size_t)row * a.ldkv + (n - qdim - hd);
+    bf16x4 pk = {f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
+    *reinterpret_cast<bf16x4*>(dst) = pk;
+    if (a.norm_factor && nt == 0 && nf_writer) a.norm_factor[row] = f2bf(f);
+    return;
+  }
+  bf16x4 pk = {f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
+  *reinterpret_cast<bf16x4*>(a.out + (size_t)row * a.ldo + n) = pk;
+}
+
 template <int EPI, bool DUAL, int KTW>
 __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   constexpr int ND = DUAL ? 2 : 1;
@@ -57,10 +122,10 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   constexpr int KW = KTW * 32;            // k columns per wave
   constexpr int XP = KW + 8;              // bf16 pitch of a staged x row (16 B pad: conflict-free reads)
   constexpr int CHUNKS = KW / 8;          // 16-byte chunks per staged row
+  constexpr int XIT = (64 * CHUNKS) / PI0_WAVE;
   constexpr size_t X_BYTES = 4 * 64 * XP * 2;
   constexpr size_t R_BYTES = (ND * 4 * 4 * 4 * PI0_WAVE + 4 * 4 * PI0_WAVE) * 4;
   __shared__ __attribute__((aligned(16))) char smem[X_BYTES > R_BYTES ? X_BYTES : R_BYTES];
-  __shared__ int s_last;
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int splitk = a.splitk;
@@ -71,21 +136,22 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   const int KT = a.K >> 5;
   const int kt0 = ks * (KT / splitk) + wave * KTW;
 
-  // ---- stage this wave's x slice [rows x KW] in LDS with coalesced 16-byte loads.
-  // Chunk indices past the last row re-load the last chunk (unconditional loads,
-  // all in flight); LDS rows >= `rows` are never written and only reach output
-  // rows that are never stored.
+  // ---- stage this wave's x slice [64 x KW] in LDS with coalesced 16-byte loads.
+  // The buffer resource ends after row `rows`: rows past M load as zeros.
   __bf16* xs = reinterpret_cast<__bf16*>(smem) + wave * 64 * XP;
   bf16x8 b0[KTW], b1[KTW];
+  PI0_PROBE(0);
   {
-    const int total = rows * CHUNKS;
-    bf16x8 xv[(64 * CHUNKS) / PI0_WAVE];
+    constexpr int RPI = PI0_WAVE / CHUNKS;            // rows covered per load instruction
+    const __amdgpu_buffer_rsrc_t xr =
+        rows_rsrc(a.x + (size_t)m0 * a.ldx, rows * a.ldx * (int)sizeof(__bf16));
+    const int lrow0 = lane / CHUNKS, lch = lane % CHUNKS;
+    const int voff = (lrow0 * a.ldx + kt0 * 32 + lch * 8) * (int)sizeof(__bf16);
+    const int vstep = RPI * a.ldx * (int)sizeof(__bf16);
+    bf16x8 xv[XIT];
 #pragma unroll
-    for (int it = 0; it < (64 * CHUNKS) / PI0_WAVE; ++it) {
-      const int idx = min(it * PI0_WAVE + lane, total - 1);
-      const int row = idx / CHUNKS, ch = idx - row * CHUNKS;
-      xv[it] = load8(a.x + (size_t)(m0 + row) * a.ldx + kt0 * 32 + ch * 8);
-    }
+    for (int it = 0; it < XIT; ++it) xv[it] = buf_load8(xr, voff + it * vstep);
+    PI0_PROBE(1);
     // weight stream, issued after the (L2-resident) x loads: loads return in
     // order, so x is usable as soon as it lands and each MFMA waits only for
     // the weight fragments it consumes. All fragments of the wave in flight.
@@ -99,12 +165,10 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
         for (int i = 0; i < KTW; ++i) b1[i] = load8(wq + i * 512);
       }
     }
+    PI0_PROBE(2);
+    __bf16* xl = xs + lrow0 * XP + lch * 8;
 #pragma unroll
-    for (int it = 0; it < (64 * CHUNKS) / PI0_WAVE; ++it) {
-      const int idx = min(it * PI0_WAVE + lane, total - 1);
-      const int row = idx / CHUNKS, ch = idx - row * CHUNKS;
-      *reinterpret_cast<bf16x8*>(xs + row * XP + ch * 8) = xv[it];
-    }
+    for (int it = 0; it < XIT; ++it) *reinterpret_cast<bf16x8*>(xl + it * RPI * XP) = xv[it];
   }
   // (each wave reads only the rows it staged itself: no workgroup barrier needed)
 
@@ -165,106 +229,57 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
       for (int q = 0; q < 4; ++q) ss += ssred[w][mt][q * 16 + r16];
   }
 
-  // ---- split-K across workgroups: last arrival sums partials in split order
+  // ---- split-K across workgroups: publish the fp32 partial tile (plain stores; the
+  // kernel boundary orders them before splitk_reduce_kernel, which sums the splits
+  // in order -- deterministic -- and runs the epilogue)
   if (splitk > 1) {
     const int tile = mb * ntiles + nt;
     const size_t tiles = (size_t)gridDim.y * ntiles;
-    // partial tile layout: [tile][split][64 rows][16 * ND] fp32, then [tile][split][64] sums
-    const __amdgpu_buffer_rsrc_t rs = dev_rsrc(a.ws);
-    const int ss_base = (int)(part_floats((int)tiles, splitk, ND) * 4);
-    {
-      const int off = (int)((((size_t)tile * splitk + ks) * 64 + lrow) * 16 * ND + c4) * 4;
-      dev_store4(rs, off, f32x4{v0[0], v0[1], v0[2], v0[3]});
-      if constexpr (DUAL) dev_store4(rs, off + 64, f32x4{v1[0], v1[1], v1[2], v1[3]});
-      if (RMS && (t & 3) == 0)
-        dev_store1(rs, ss_base + (int)(((size_t)tile * splitk + ks) * 64 + lrow) * 4, ss);
-    }
-    if (!arrive_last(a.counters + tile, splitk, &s_last)) return;
-    // all partial loads in flight together (splitk <= MAX_SPLITK), summed in split order
-    f32x4 q0[MAX_SPLITK], q1[MAX_SPLITK];
-    float qs[MAX_SPLITK];
-#pragma unroll
-    for (int k = 0; k < MAX_SPLITK; ++k) {
-      const int kk = min(k, splitk - 1);     // unconditional loads; extra ones are ignored
-      const int off = (int)((((size_t)tile * splitk + kk) * 64 + lrow) * 16 * ND + c4) * 4;
-      q0[k] = dev_load4(rs, off);
-      if constexpr (DUAL) q1[k] = dev_load4(rs, off + 64);
-      if constexpr (RMS) qs[k] = dev_load1(rs, ss_base + (int)(((size_t)tile * splitk + kk) * 64 + lrow) * 4);
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) { v0[c] = 0.f; v1[c] = 0.f; }
-    ss = 0.f;
-#pragma unroll
-    for (int k = 0; k < MAX_SPLITK; ++k) {
-      if (k < splitk) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) v0[c] += q0[k][c];
-        if constexpr (DUAL) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) v1[c] += q1[k][c];
-        }
-        if constexpr (RMS) ss += qs[k];
-      }
-    }
-  }
-
-  // ---- epilogue
-  const int row = m0 + lrow;
-  if (row >= a.M) return;
-  const int n = nt * 16 + c4;
-  float f = 1.f;
-  if constexpr (RMS) f = round_bf(rsqrtf(ss / (float)a.K + 1e-6f));
-
-  float o[4];
-  if constexpr (EPI == EPI_BIAS) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) o[c] = v0[c] + bf2f(a.bias[n + c]);
-  } else if constexpr (EPI == EPI_RES) {
-    const __bf16* rp = a.out + (size_t)row * a.ldo + n;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) o[c] = v0[c] + bf2f(rp[c]);
-  } else if constexpr (EPI == EPI_RMS_BIAS_RES) {
-    if (a.out_f32) {            // fp32 Euler accumulator: read, update and store in fp32
-      float* rp = a.out_f32 + (size_t)row * a.ldo + n;
-      const f32x4 r4 = *reinterpret_cast<const f32x4*>(rp);
-      f32x4 o4;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) o4[c] = v0[c] * f + bf2f(a.bias[n + c]) + r4[c];
-      *reinterpret_cast<f32x4*>(rp) = o4;
-      return;
-    }
-    const __bf16* rp = a.out + (size_t)row * a.ldo + n;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) o[c] = v0[c] * f + bf2f(a.bias[n + c]) + bf2f(rp[c]);
-  } else if constexpr (EPI == EPI_GATE) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) o[c] = gelu_tanh(v0[c] * f) * (v1[c] * f);
-  } else if constexpr (EPI == EPI_QKV_ROPE) {
-    const int hd = a.head_dim, qdim = a.heads * hd;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) o[c] = v0[c] * f;
-    if (n < qdim + hd) {
-      const int rj = n % hd;
-      const __bf16* rp = a.rope + (size_t)row * hd + rj;
-#pragma unroll
-      for (int p = 0; p < 4; p += 2) {
-        const float cs = bf2f(rp[p]), sn = bf2f(rp[p + 1]);
-        const float x0 = o[p], x1 = o[p + 1];
-        o[p] = x0 * cs - x1 * sn;
-        o[p + 1] = x1 * cs + x0 * sn;
-      }
-    }
-    __bf16* dst;
-    if (n < qdim) dst = a.out + (size_t)row * qdim + n;
-    else if (n < qdim + hd) dst = a.out_k + (size_t)row * a.ldkv + (n - qdim);
-    else dst = a.out_v + (size_t)row * a.ldkv + (n - qdim - hd);
-    bf16x4 pk = {f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
-    *reinterpret_cast<bf16x4*>(dst) = pk;
-    if (a.norm_factor && nt == 0 && (t & 3) == 0) a.norm_factor[row] = f2bf(f);
+    float* p = a.ws + (((size_t)tile * splitk + ks) * 64 + lrow) * 16 * ND + c4;
+    *reinterpret_cast<f32x4*>(p) = f32x4{v0[0], v0[1], v0[2], v0[3]};
+    if constexpr (DUAL) *reinterpret_cast<f32x4*>(p + 16) = f32x4{v1[0], v1[1], v1[2], v1[3]};
+    if (RMS && (t & 3) == 0)
+      a.ws[part_floats((int)tiles, splitk, ND) + ((size_t)tile * splitk + ks) * 64 + lrow] = ss;
     return;
   }
-  bf16x4 pk = {f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
-  *reinterpret_cast<bf16x4*>(a.out + (size_t)row * a.ldo + n) = pk;
+  gemm_epilogue<EPI, DUAL>(a, m0 + lrow, nt, c4, (t & 3) == 0, v0, v1, ss);
+}
+
+
+// Second pass of split-K: one workgroup per 64 x 16 output tile; thread t owns row
+// t/4, columns 4*(t%4)..; sums the splits in split order, then the epilogue.
+template <int EPI, bool DUAL>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a) {
+  constexpr int ND = DUAL ? 2 : 1;
+  constexpr bool RMS = uses_rms(EPI);
+  const int t = threadIdx.x, lrow = t >> 2, c4 = (t & 3) * 4;
+  const int nt = blockIdx.x, mb = blockIdx.y, ntiles = gridDim.x;
+  const int tile = mb * ntiles + nt, splitk = a.splitk;
+  const size_t tiles = (size_t)gridDim.y * ntiles;
+  f32x4 q0[MAX_SPLITK], q1[MAX_SPLITK];
+  float qs[MAX_SPLITK];
+#pragma unroll
+  for (int k = 0; k < MAX_SPLITK; ++k) {     // unconditional loads; extra ones are ignored
+    const int kk = min(k, splitk - 1);
+    const float* p = a.ws + (((size_t)tile * splitk + kk) * 64 + lrow) * 16 * ND + c4;
+    q0[k] = *reinterpret_cast<const f32x4*>(p);
+    if constexpr (DUAL) q1[k] = *reinterpret_cast<const f32x4*>(p + 16);
+    if constexpr (RMS) qs[k] = a.ws[part_floats((int)tiles, splitk, ND) + ((size_t)tile * splitk + kk) * 64 + lrow];
+  }
+  float v0[4] = {0.f, 0.f, 0.f, 0.f}, v1[4] = {0.f, 0.f, 0.f, 0.f}, ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < MAX_SPLITK; ++k) {
+    if (k < splitk) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v0[c] += q0[k][c];
+      if constexpr (DUAL) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v1[c] += q1[k][c];
+      }
+      if constexpr (RMS) ss += qs[k];
+    }
+  }
+  gemm_epilogue<EPI, DUAL>(a, mb * 64 + lrow, nt, c4, (t & 3) == 0, v0, v1, ss);
 }
 
 template <int EPI, bool DUAL>
@@ -273,7 +288,7 @@ static int launch_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.K % 32 || a.N % 16 || a.splitk < 1 || a.splitk > MAX_SPLITK) return PI0HIP_ERR_SHAPE;
   const int KT = a.K / 32;
   if (KT % (4 * a.splitk)) return PI0HIP_ERR_SHAPE;
-  if (a.splitk > 1 && (!a.ws || !a.counters)) return PI0HIP_ERR_WORKSPACE;
+  if (a.splitk > 1 && !a.ws) return PI0HIP_ERR_WORKSPACE;
   const int ktw = KT / (4 * a.splitk);
   dim3 grid((a.N / 16) * a.splitk, (a.M + 63) / 64);
   switch (ktw) {
@@ -282,6 +297,11 @@ static int launch_gemm(const GemmArgs& a, hipStream_t s) {
     case 4: skinny_gemm_kernel<EPI, DUAL, 4><<<grid, 256, 0, s>>>(a); break;
     case 8: skinny_gemm_kernel<EPI, DUAL, 8><<<grid, 256, 0, s>>>(a); break;
     default: return PI0HIP_ERR_SHAPE;
+  }
+  if (a.splitk > 1) {
+    if (hipError_t e = hipGetLastError()) return (int)e;
+    hipLaunchKernelGGL((splitk_reduce_kernel<EPI, DUAL>), dim3(a.N / 16, (a.M + 63) / 64),
+                       dim3(256), 0, s, a);
   }
   return (int)hipGetLastError();
 }
@@ -320,16 +340,14 @@ size_t pi0hip_gemm_workspace_bytes(int M, int N, int splitk, int dual) {
   const size_t tiles = (size_t)((M + 63) / 64) * (N / 16);
   const int nd = dual ? 2 : 1;
   const size_t floats = part_floats((int)tiles, splitk, nd) + tiles * splitk * 64;
-  return round_up(tiles * sizeof(int), 256) + floats * sizeof(float);
+  return floats * sizeof(float);
 }
 
 static int setup_ws(GemmArgs& a, void* ws, size_t ws_bytes, int dual) {
-  if (a.splitk <= 1) { a.ws = nullptr; a.counters = nullptr; return 0; }
+  if (a.splitk <= 1) { a.ws = nullptr; return 0; }
   const size_t need = pi0hip_gemm_workspace_bytes(a.M, a.N, a.splitk, dual);
   if (!ws || ws_bytes < need) return PI0HIP_ERR_WORKSPACE;
-  const size_t tiles = (size_t)((a.M + 63) / 64) * (a.N / 16);
-  a.counters = reinterpret_cast<int*>(ws);
-  a.ws = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + round_up(tiles * sizeof(int), 256));
+  a.ws = reinterpret_cast<float*>(ws);
   return 0;
 }
 

@@ -2,9 +2,7 @@
 
 Each (role, shape, dtype, device) buffer is allocated once, zeroed, and reused.
 After warmup the pool is frozen: a request that warmup did not cover raises
-instead of allocating inside a hipGraph capture. Zeroing matters here: the
-split-K GEMMs keep arrival counters in their workspace and expect them to
-start (and they leave them) at zero.
+instead of allocating inside a hipGraph capture.
 """
 from __future__ import annotations
 

@@ -37,8 +37,8 @@ int pi0hip_version(void);
  * TMA); this is the one-time relayout that makes the weight stream coalesced. */
 int pi0hip_pack_weight(const void* w, void* packed, int K, int N, int batch, hipStream_t s);
 
-/* Workspace for the split-K GEMMs (0 when splitk == 1). Counters inside must
- * start zeroed; the kernels leave them zeroed again. */
+/* Workspace for the split-K GEMMs (0 when splitk == 1): fp32 partial tiles
+ * written by the GEMM launch and summed by its second (reduce) launch. */
 size_t pi0hip_gemm_workspace_bytes(int M, int N, int splitk, int dual);
 
 /* out[m, n] = act(x[m, :K] @ w[K, N] + bias[n]); act 0 = identity, 1 = silu.

@@ -38,12 +38,12 @@ def test_workspace_sizes_are_host_computable():
     assert lib.pi0hip_version() >= 1
     assert lib.pi0hip_gemm_workspace_bytes(51, 1024, 1, 0) == 0
     ws = lib.pi0hip_gemm_workspace_bytes(51, 1024, 4, 0)
-    # 64 tiles x 4 splits x (64x16 partials + 64 sums) floats + 64 counters (padded)
-    assert ws == 256 + 64 * 4 * (64 * 16 + 64) * 4
+    # 64 tiles x 4 splits x (64x16 partials + 64 sums) floats
+    assert ws == 64 * 4 * (64 * 16 + 64) * 4
     att = lib.pi0hip_attention_workspace_bytes(408, 819)
-    # 26 tiles of 16 rows (416 padded), 7 chunks of 128 keys: counters, lse, fp32 partials
+    # 26 tiles of 16 rows (416 padded), 7 chunks of 128 keys: lse, fp32 partials
     r256 = lambda v: (v + 255) // 256 * 256
-    assert att == r256(26 * 4) + r256(7 * 416 * 4) + 7 * 416 * 256 * 4
+    assert att == r256(7 * 416 * 4) + 7 * 416 * 256 * 4
 
 
 def test_rejected_arguments_do_not_launch():
