@@ -7,7 +7,7 @@ The public names follow the reference package facade (`src/flash_vla/__init__.py
 """
 from __future__ import annotations
 
-__all__ = ["Pi0DecoderEngine", "random_checkpoint", "decoder_checkpoint", "decoder_inputs",
+__all__ = ["Pi0DecoderEngine", "Pi0EncoderEngine", "random_checkpoint", "decoder_checkpoint", "decoder_inputs",
            "op_table"]
 
 
@@ -20,6 +20,8 @@ def __getattr__(name: str):
         from .ops import op_table as value
     elif name == "Pi0DecoderEngine":
         from .engine import Pi0DecoderEngine as value
+    elif name == "Pi0EncoderEngine":
+        from .engine import Pi0EncoderEngine as value
     else:
         raise AttributeError(f"module {__name__!r} has no attribute {name!r}")
     globals()[name] = value

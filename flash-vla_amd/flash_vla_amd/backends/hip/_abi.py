@@ -11,7 +11,7 @@ import os
 _LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.dirname(
     os.path.abspath(__file__)))), "lib", "libpi0hip.so")
 
-c_int, c_size_t, c_void_p = ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p
+c_int, c_size_t, c_void_p, c_float = ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_float
 P = c_void_p
 
 # name -> (restype, argtypes); must match include/pi0_hip.h exactly.
@@ -35,6 +35,18 @@ PROTOTYPES = {
     "pi0hip_attention_workspace_bytes": (c_size_t, [c_int, c_int]),
     "pi0hip_attention": (c_int, [P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int, c_int,
                                  c_int, P, c_size_t, P]),
+    # prefix encoder
+    "pi0hip_rms_norm": (c_int, [P, c_int, P, c_int, c_int, c_int, P]),
+    "pi0hip_layer_norm": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_float, P]),
+    "pi0hip_tile_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "pi0hip_tile_linear": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, P]),
+    "pi0hip_tile_linear_residual": (c_int, [P, c_int, P, P, c_int, c_int, c_int, c_int, c_int,
+                                            P, c_size_t, P]),
+    "pi0hip_tile_gated_ffn": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, P]),
+    "pi0hip_tile_qkv_rope": (c_int, [P, c_int, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int,
+                                     P]),
+    "pi0hip_encoder_attention": (c_int, [P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int,
+                                         c_float, P]),
 }
 
 ERRORS = {-1: "invalid argument", -2: "unsupported shape", -3: "workspace missing or too small"}

@@ -115,10 +115,12 @@ def packed_weight_ptr(w: torch.Tensor) -> int:
 
 
 def prepare_weights(weights: dict) -> None:
-    """Pack every 2-D/3-D GEMM weight of the decoder up front (outside any capture)."""
+    """Pack every 2-D/3-D GEMM weight of the decoder and encoder up front (outside any capture)."""
     for name in ("decoder_action_mlp_w", "decoder_attn_qkv_w", "decoder_attn_o_w",
                  "decoder_ffn_gate_w", "decoder_ffn_up_w", "decoder_ffn_down_w",
-                 "decoder_action_fused_out_proj_w"):
+                 "decoder_action_fused_out_proj_w", "encoder_multi_modal_projector_w",
+                 "encoder_attn_qkv_w", "encoder_attn_o_w", "encoder_ffn_gate_w",
+                 "encoder_ffn_up_w", "encoder_ffn_down_w"):
         if name in weights:
             w = weights[name]
             packed_weight_ptr(w if w.dim() == 2 else w[0])

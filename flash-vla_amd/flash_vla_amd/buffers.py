@@ -7,12 +7,18 @@ in place):
   decoder_q_buf          [(chunk + 1) * 8, 256]          flat (token * 8 + head) queries,
                                                          reused as the attention output
   decoder_hidden         [chunk + 1, 4096]               GeGLU activations
+Encoder (prefix) buffers, M = encoder_seq_len token rows:
+  encoder_x / encoder_x_norm  [M, 2048]      residual stream / its RMS-normalised copy
+  encoder_Q                   [M * 8, 256]   flat queries (token * 8 + head)
+  encoder_hidden              [M, 16384]     GeGLU activations
+  encoder_rope_weights        [M, 256]       positions 0 .. M - 1
 """
 from __future__ import annotations
 
 import torch
 
-from .spec import DECODER_FFN, DECODER_HEADS, DECODER_LAYERS, DECODER_WIDTH, HEAD_DIM, ROPE_THETA
+from .spec import (DECODER_FFN, DECODER_HEADS, DECODER_LAYERS, DECODER_WIDTH, ENCODER_FFN,
+                   ENCODER_LAYERS, ENCODER_WIDTH, HEAD_DIM, ROPE_THETA, VISION_WIDTH)
 
 
 def rope_table(seq_len: int, offset: int, head_dim: int, device) -> torch.Tensor:
@@ -53,4 +59,33 @@ def allocate_decoder_buffers(encoder_seq_len: int, chunk_size: int, device,
         "decoder_hidden": buf(dec_len, ffn),
     }
     buffers["decoder_rope_weights"].copy_(rope_table(dec_len, encoder_seq_len, head_dim, device))
+    return buffers
+
+
+def allocate_encoder_buffers(encoder_seq_len: int, device, buffers: dict | None = None,
+                             layers: int = ENCODER_LAYERS, width: int = ENCODER_WIDTH,
+                             ffn: int = ENCODER_FFN, heads: int = DECODER_HEADS,
+                             head_dim: int = HEAD_DIM, cache_len: int | None = None,
+                             num_views: int = 3) -> dict:
+    """The encoder part of `buffers.py:37-64`; adds to `buffers` (sharing its K/V cache)."""
+    bf16 = torch.bfloat16
+    buffers = {} if buffers is None else buffers
+    if cache_len is None:
+        cache_len = encoder_seq_len
+
+    def buf(*shape):
+        return torch.zeros(shape, dtype=bf16, device=device)
+
+    buffers.update({
+        "encoder_rope_weights": buf(encoder_seq_len, head_dim),
+        "encoder_x": buf(encoder_seq_len, width),
+        "encoder_x_norm": buf(encoder_seq_len, width),
+        "encoder_Q": buf(encoder_seq_len * heads, head_dim),
+        "encoder_hidden": buf(encoder_seq_len, ffn),
+        "vision_x_norm": buf(num_views, 256, VISION_WIDTH),
+    })
+    if "encoder_K" not in buffers:
+        buffers["encoder_K"] = buf(layers, cache_len, head_dim)
+        buffers["encoder_V"] = buf(layers, cache_len, head_dim)
+    buffers["encoder_rope_weights"].copy_(rope_table(encoder_seq_len, 0, head_dim, device))
     return buffers

@@ -7,7 +7,9 @@ and the packed-weight cache), freeze the pool, capture one graph on a side
 stream; `forward` copies the inputs into their static buffers and replays.
 The prefix KV cache (the encoder's output) is supplied by the caller through
 `load_prefix`; the vision and prefix-encoder stages are not part of this
-engine.
+engine. `Pi0EncoderEngine` is the same discipline for the prefix encoder
+(`pipeline.py:57-89`): its input is the [M, 2048] encoder activation, its
+output the K/V cache rows the decoder attends over.
 """
 from __future__ import annotations
 
@@ -16,7 +18,7 @@ import torch
 from . import pipeline
 from .arena import ScratchPool
 from .backends import BACKENDS
-from .buffers import allocate_decoder_buffers
+from .buffers import allocate_decoder_buffers, allocate_encoder_buffers
 from .ops import op_table
 from .spec import DECODER_WEIGHT_NAMES, decoder_weight_shapes
 
@@ -112,6 +114,77 @@ class Pi0DecoderEngine:
 
     def replay(self) -> None:
         """Replay the captured loop on whatever the static buffers hold (benchmarks)."""
+        self.graph.replay()
+
+
+class Pi0EncoderEngine:
+    """The captured prefix encoder: [M, 2048] input rows -> K/V cache rows of every layer."""
+
+    WEIGHTS = ("encoder_attn_qkv_w", "encoder_attn_o_w", "encoder_ffn_gate_w",
+               "encoder_ffn_up_w", "encoder_ffn_down_w")
+
+    def __init__(self, weights: dict, encoder_seq_len: int = 768, layers: int | None = None,
+                 backend: str = "hip", plan: dict | None = None, device: str = "cuda",
+                 capture: bool = True, warmup: int = 2, cache_len: int | None = None,
+                 copy_weights: bool = True):
+        self.encoder_seq_len = encoder_seq_len
+        self.ops = op_table(True, backend=backend, plan=plan)
+        self.backend = BACKENDS[backend]
+        n_layers = weights["encoder_attn_qkv_w"].shape[0]
+        self.layers = n_layers if layers is None else layers
+        if self.layers > n_layers:
+            raise ValueError(f"layers={layers} but the checkpoint has {n_layers}")
+        self.weights = {}
+        for name in self.WEIGHTS:
+            w = weights[name]
+            if copy_weights or w.device != torch.device(device) or w.dtype != torch.bfloat16:
+                w = w.to(device=device, dtype=torch.bfloat16).contiguous()
+            self.weights[name] = w
+        qkv, o = self.weights["encoder_attn_qkv_w"], self.weights["encoder_attn_o_w"]
+        head_dim = (qkv.shape[2] - o.shape[1]) // 2
+        self.buffers = allocate_encoder_buffers(
+            encoder_seq_len, device, layers=n_layers, width=qkv.shape[1],
+            ffn=self.weights["encoder_ffn_gate_w"].shape[2], heads=o.shape[1] // head_dim,
+            head_dim=head_dim, cache_len=cache_len)
+        self.pool = ScratchPool()
+        self.graph = None
+        if hasattr(self.backend, "prepare_weights"):
+            self.backend.prepare_weights(self.weights)
+        if capture:
+            self._capture(warmup)
+
+    def _run(self):
+        with self.backend.use_pool(self.pool):
+            pipeline.transformer_encoder(self.ops, self.weights, self.buffers,
+                                         self.encoder_seq_len, layers=self.layers, project=False)
+
+    def _capture(self, warmup: int):
+        saved = self.buffers["encoder_x"].clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                self.buffers["encoder_x"].copy_(saved)
+                self._run()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self.pool.freeze()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._run()
+        torch.cuda.synchronize()
+        self.buffers["encoder_x"].copy_(saved)
+
+    def forward(self, x: torch.Tensor):
+        """Run the encoder on `x` ([M, width]); returns (encoder_K, encoder_V) static buffers."""
+        self.buffers["encoder_x"].copy_(x)
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self._run()
+        return self.buffers["encoder_K"], self.buffers["encoder_V"]
+
+    def replay(self) -> None:
         self.graph.replay()
 
 

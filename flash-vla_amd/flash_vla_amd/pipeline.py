@@ -1,4 +1,4 @@
-"""The decoder execution plan (mirrors `hardware/nvidia/h100/pi0/pipeline.py:92-135`).
+"""The encoder and decoder execution plans (mirror `hardware/nvidia/h100/pi0/pipeline.py:57-135`).
 
 Pure orchestration: every line is an op-table call on static buffers, so the
 loop captures into one hipGraph. Sequence = one state token + the action
@@ -11,6 +11,44 @@ rounded into the bf16 `diffusion_noise` once, after the last step; otherwise
 the bf16 buffer itself is updated every step, as in the reference.
 """
 from __future__ import annotations
+
+from .spec import HEAD_DIM
+
+
+def transformer_encoder(ops, weights, buffers, encoder_seq_len, layers=18, project=True):
+    """Prefix encoder (pipeline.py:57-89): optional vision projector, then the Gemma layers.
+
+    The last layer runs only its norm + QKV + RoPE: only its K and V are read
+    (by the decoder). `project=False` starts from an `encoder_x` already in
+    place (the config-3 workload, whose input is the [M, 2048] activation).
+    `ops.encoder_attention` is the op-table form of the function the
+    reference pipeline calls directly (`kernels/attention.py:29-34`).
+    """
+    if project:
+        ops.encoder_projector(
+            buffers["vision_x"],
+            weights["vision_final_norm_w"], weights["vision_final_norm_b"],
+            weights["encoder_multi_modal_projector_w"], weights["encoder_multi_modal_projector_b"],
+            buffers["encoder_x"], buffers["vision_x_norm"])
+
+    scale = HEAD_DIM ** -0.5
+    for i in range(layers):
+        ops.encoder_norm_qkv_rope(
+            buffers["encoder_x"], weights["encoder_attn_qkv_w"][i],
+            buffers["encoder_rope_weights"], buffers["encoder_Q"],
+            buffers["encoder_K"][i, :encoder_seq_len], buffers["encoder_V"][i, :encoder_seq_len],
+            buffers["encoder_x_norm"])
+        if i == layers - 1:
+            break
+        attn = ops.encoder_attention(
+            buffers["encoder_Q"], buffers["encoder_K"][i, :encoder_seq_len],
+            buffers["encoder_V"][i, :encoder_seq_len], scale)
+        ops.encoder_out_proj_residual(attn, weights["encoder_attn_o_w"][i], buffers["encoder_x"])
+        ops.encoder_norm_gated_ffn(
+            buffers["encoder_x"], weights["encoder_ffn_gate_w"][i], weights["encoder_ffn_up_w"][i],
+            buffers["encoder_hidden"], buffers["encoder_x_norm"])
+        ops.encoder_ffn_down_residual(
+            buffers["encoder_hidden"], weights["encoder_ffn_down_w"][i], buffers["encoder_x"])
 
 
 def transformer_decoder(ops, weights, buffers, encoder_seq_len, steps=10, layers=18):

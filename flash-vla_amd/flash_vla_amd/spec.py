@@ -14,6 +14,10 @@ HEAD_DIM = 256
 DECODER_HEADS = 8
 ROPE_THETA = 10000
 DECODER_WIDTH = 1024
+ENCODER_WIDTH = 2048
+ENCODER_FFN = 16384
+VISION_WIDTH = 1152
+VISION_TOKENS = 256
 DECODER_FFN = 4096
 ACTION_DIM = 32
 NUM_STEPS = 10

@@ -21,7 +21,7 @@ import math
 import torch
 
 from .spec import (ACTION_DIM, DECODER_FFN, DECODER_HEADS, DECODER_LAYERS, DECODER_WIDTH,
-                   HEAD_DIM, NUM_STEPS, weight_shapes)
+                   ENCODER_FFN, ENCODER_LAYERS, ENCODER_WIDTH, HEAD_DIM, NUM_STEPS, weight_shapes)
 
 EULER_DT = -0.1
 TIME_MIN_PERIOD = 4e-3
@@ -188,3 +188,44 @@ def decoder_inputs(seed: int = 1, encoder_seq_len: int = 768, chunk_size: int = 
     return {"observation_state_normalized": state.to(device),
             "diffusion_noise": noise.to(device),
             "encoder_K": k.to(device), "encoder_V": v.to(device)}
+
+
+ENCODER_WEIGHT_NAMES = ("encoder_attn_qkv_w", "encoder_attn_o_w", "encoder_ffn_gate_w",
+                        "encoder_ffn_up_w", "encoder_ffn_down_w")
+
+
+def encoder_checkpoint(seed: int = 2, std: float = 0.02, layers: int = ENCODER_LAYERS,
+                       width: int = ENCODER_WIDTH, ffn: int = ENCODER_FFN,
+                       heads: int = DECODER_HEADS, head_dim: int = HEAD_DIM,
+                       device: str = "cpu") -> dict:
+    """Packed prefix-encoder tensors, N(0, std) per element.
+
+    With Gemma RMSNorm weights 0 the fold of `fold_decoder` multiplies the
+    projections by 1 and only permutes Q/K columns, which leaves i.i.d. normal
+    entries i.i.d. normal: drawing the packed tensors directly gives the same
+    distribution (the fold algebra itself is pinned against the unfolded layer
+    at small size by the oracle tests). Drawn layer by layer on the CPU
+    generator, rounded to bf16 at once, so the 18-layer set (~4 GB) never exists
+    in fp32.
+    """
+    gen = _gen(seed)
+    shapes = {
+        "encoder_attn_qkv_w": (width, (heads + 2) * head_dim),
+        "encoder_attn_o_w": (heads * head_dim, width),
+        "encoder_ffn_gate_w": (width, ffn),
+        "encoder_ffn_up_w": (width, ffn),
+        "encoder_ffn_down_w": (ffn, width),
+    }
+    out = {n: torch.empty((layers, *sh), dtype=torch.bfloat16, device=device)
+           for n, sh in shapes.items()}
+    for i in range(layers):
+        for n, sh in shapes.items():
+            out[n][i].copy_((torch.randn(sh, generator=gen) * std).to(torch.bfloat16))
+    return out
+
+
+def encoder_inputs(seed: int = 3, encoder_seq_len: int = 768, width: int = ENCODER_WIDTH,
+                   device: str = "cpu") -> torch.Tensor:
+    """The config-3 encoder input: a seeded N(0, 1) bf16 [encoder_seq_len, width] activation."""
+    gen = _gen(seed)
+    return torch.randn(encoder_seq_len, width, generator=gen).to(torch.bfloat16).to(device)

@@ -106,6 +106,59 @@ int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int l
                      int ldo, int rows, int keys, int enc_len, int heads, int head_dim,
                      void* ws, size_t ws_bytes, hipStream_t s);
 
+/* ---- prefix encoder (M = 768..816 token rows, width 2048) --------------------
+ * LDS-tiled MFMA GEMMs for the MFMA-bound encoder shapes; weights packed by
+ * pi0hip_pack_weight, K % 64 == 0. */
+
+/* out = bf16(x * rsqrt(mean(x^2) + 1e-6)), one row per wave; K in {1024, 2048}.
+ * tl_rms_norm, kernels/base.py:373-403 (encoder_norm_qkv_rope / encoder_norm_gated_ffn,
+ * wrappers.py:347-381) */
+int pi0hip_rms_norm(const void* x, int ldx, void* out, int ldo, int M, int K, hipStream_t s);
+
+/* fp32 split-K partials of pi0hip_tile_linear_residual (0 when splitk == 1). */
+size_t pi0hip_tile_workspace_bytes(int M, int N, int splitk);
+
+/* out = x @ W (+ bias[n] when bias != NULL); N % 128 == 0.
+ * encoder_projector GEMM, wrappers.py:336-344 (tl_matmul_bias, kernels/base.py:158-192) */
+int pi0hip_tile_linear(const void* x, int ldx, const void* w_packed, const void* bias, void* out,
+                       int ldo, int M, int N, int K, hipStream_t s);
+
+/* out += x @ W in place, one bf16 rounding; splitk > 1 sums fp32 partials in a
+ * second launch (K / 64 divisible by splitk). N % 128 == 0.
+ * encoder_out_proj_residual wrappers.py:366-371, encoder_ffn_down_residual
+ * wrappers.py:383-392 (tl_matmul_res_ws, kernels/base.py:115-155) */
+int pi0hip_tile_linear_residual(const void* x, int ldx, const void* w_packed, void* out, int ldo,
+                                int M, int N, int K, int splitk, void* ws, size_t ws_bytes,
+                                hipStream_t s);
+
+/* out = bf16(gelu_tanh(x @ Wg) * (x @ Wu)) on fp32 accumulators; N % 128 == 0.
+ * encoder_norm_gated_ffn GEMM, wrappers.py:374-380 (tl_matmul_gate, kernels/base.py:508-549) */
+int pi0hip_tile_gated_ffn(const void* x, int ldx, const void* gate_packed, const void* up_packed,
+                          void* out, int ldo, int M, int N, int K, hipStream_t s);
+
+/* proj = bf16(x @ W), W = [K, (heads + 2) * head_dim]; RoPE (interleaved pairs,
+ * table rope[M, head_dim]) on the rounded Q and K columns, then scatter to
+ * q [M, heads*head_dim], k / v rows [M, ldkv].
+ * encoder_norm_qkv_rope GEMM + scatter, wrappers.py:347-363 (tl_matmul_ws +
+ * tl_rope_scatter_bf16, kernels/base.py:112, 672-726) */
+int pi0hip_tile_qkv_rope(const void* x, int ldx, const void* w_packed, const void* rope, void* q,
+                         void* k, void* v, int ldkv, int M, int K, int heads, int head_dim,
+                         hipStream_t s);
+
+/* out = bf16((x - mean) * rsqrt(var + eps) * w + b), var = E[x^2] - mean^2 in fp32;
+ * K % 8 == 0, K <= 2048.
+ * encoder_projector's vision final norm, wrappers.py:336-344 (tl_layer_norm,
+ * kernels/base.py:405-447) */
+int pi0hip_layer_norm(const void* x, int ldx, const void* w, const void* b, void* out, int ldo,
+                      int M, int K, float eps, hipStream_t s);
+
+/* out = softmax(scale * bf16(q k^T)) v, every flat query row over every key
+ * (one shared KV head, no mask); head_dim must be 256. `out` must not alias q.
+ * encoder_attention, kernels/attention.py:29-34 */
+int pi0hip_encoder_attention(const void* q, int ldq, const void* k, const void* v, int ldkv,
+                             void* out, int ldo, int rows, int keys, int head_dim, float scale,
+                             hipStream_t s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -63,13 +63,17 @@ def test_rejected_arguments_do_not_launch():
         _abi.check(-2, "x")
 
 
+ENCODER_OPS = {"encoder_projector", "encoder_norm_qkv_rope", "encoder_out_proj_residual",
+               "encoder_norm_gated_ffn", "encoder_ffn_down_residual", "encoder_attention"}
+
+
 def test_op_table_contract():
     t = op_table(fused=True)
-    assert set(vars(t)) == DECODER_OPS
+    assert set(vars(t)) == DECODER_OPS | ENCODER_OPS
     hip = BACKENDS["hip"]
     assert t.decoder_attention is hip.FUSED_WRAPPERS["decoder_attention"]
     t2 = op_table(fused=False, plan={"decoder_attention": "hip"})
-    assert set(vars(t2)) == DECODER_OPS
+    assert set(vars(t2)) == DECODER_OPS | ENCODER_OPS
     with pytest.raises(KeyError):
         op_table(plan={"not_an_op": "hip"})
     with pytest.raises(KeyError):
