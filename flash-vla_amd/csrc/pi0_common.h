@@ -16,6 +16,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 #define PI0_WAVE 64
@@ -64,6 +65,21 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v));
 // offsets stay 32-bit (row * pitch + column, plus per-iteration immediates).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, int nbytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nbytes, 0x00020000);
+}
+// The same resource built from readfirstlane'd values: provably wave-uniform, so it
+// lives in SGPRs (instructions that take it need no per-lane waterfall loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc_sgpr(const void* base, int nbytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(p >> 32));
+  void* q = reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(q, 0, __builtin_amdgcn_readfirstlane(nbytes), 0x00020000);
+}
+// 16 bytes per lane from a buffer resource straight into LDS: lane l writes
+// lds_base + 16 l (lds_base must be wave-uniform). Completion is counted by vmcnt.
+__device__ __forceinline__ void buf_load16_lds(__amdgpu_buffer_rsrc_t r, void* lds_base, int off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base,
+                                           16, off, 0, 0, 0);
 }
 __device__ __forceinline__ bf16x8 buf_load8(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));

@@ -45,118 +45,145 @@ struct TileArgs {
   int xcd_remap;
 };
 
-template <int BM, int BN, int EPI, bool DUAL>
-__global__ __launch_bounds__(256, 1) void tile_gemm_kernel(TileArgs a) {
-  constexpr int NB = BN / 16;              // B column tiles per workgroup
-  constexpr int TA = BM / 16 * 2;          // A fragments per 64-deep stage
-  constexpr int TT = TA + NB * 2;          // all fragments per stage
-  constexpr int LA = TA / 4, LT = TT / 4;  // per wave
-  constexpr int FM = BM / 32;              // row fragments per wave
-  constexpr int FN = NB / 2;               // B column tiles per wave
-  constexpr int STAGE = TT * 64;           // 16-byte slots per stage
-  static_assert(BM % 32 == 0 && BN % 32 == 0 && (!DUAL || BN % 64 == 0), "tile shape");
-  __shared__ bf16x8 lds[2 * STAGE];
+// vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt bits 3:0 and 15:14).
+#define PI0_VMCNT(n) (((n) & 0xF) | (0x7 << 4) | (0xF << 8) | (((n) >> 4) << 14))
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// v_mfma_f32_32x32x16_bf16 is used because one wave per SIMD sustains ~90% of the
+// MFMA peak with it (the 16x16x32 form stalls near 55-60% at this occupancy).
+// Fragment layouts (lane l, j = 0..7, e = 0..15):
+//   A (32 rows x 16 k): A[l % 32][8 (l / 32) + j]
+//   B (16 k x 32 cols): B[8 (l / 32) + j][l % 32]      (pi0hip_pack_weight32 order)
+//   C (32 x 32):        C[8 (e / 4) + 4 (l / 32) + e % 4][l % 32]
+//
+// Workgroup = 4 waves side by side along N; each wave owns all BM rows of the
+// block and WN of its B columns. Both operands run D 64-deep steps ahead:
+//   * A (activations, shared by the 4 waves) goes global -> LDS directly
+//     (buffer_load ... lds, 16 bytes per lane, one MFMA fragment per
+//     instruction) into a D-slot ring; the buffer resource ends at row M so the
+//     rows of a ragged last block load as zeros;
+//   * B (the packed weight stream, private to the wave) goes global -> VGPRs
+//     into a D-slot register ring, so no weight byte passes through LDS.
+// The step count is a multiple of D (the host checks), so the ring unrolls with
+// static slots; every step issues the same number of loads (steps past the end
+// re-load the last step into the free slot), so "A of step s has landed" is the
+// fixed count vmcnt <= LB + (D - 2) * (LA + LB) of loads issued after it; a plain
+// s_barrier (no fence: the fence would wait for every prefetch) then publishes it.
+template <int BM, int WN, int D, int EPI, bool DUAL, int OCC>
+__global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
+  constexpr int BN = 4 * WN;               // B columns per workgroup
+  constexpr int FM = BM / 32;              // 32-row fragments (every wave holds all rows)
+  constexpr int FN = WN / 32;              // 32-column B tiles per wave
+  constexpr int TA = FM * 4;               // A fragments per 64-deep step (4 x k16)
+  constexpr int LA = TA / 4;               // ... loaded by each wave
+  constexpr int LB = FN * 4;               // B fragments per wave per step
+  constexpr int AWAIT = LB + (D - 2) * (LA + LB);
+  constexpr int PF = 3;                    // A-fragment register ring
+  static_assert(BM % 32 == 0 && WN % 32 == 0 && (!DUAL || WN % 64 == 0), "tile shape");
+  static_assert(D >= 2 && AWAIT < 64, "pipeline depth");
+  __shared__ bf16x8 lds[D * TA * 64];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
   int id = blockIdx.x;
   if (a.xcd_remap) id = (id & 7) * (gridDim.x >> 3) + (id >> 3);
   const int mt = id % a.tiles_m;
   id /= a.tiles_m;
   const int ntile = id % a.tiles_n, ks = id / a.tiles_n;
   const int m0 = mt * BM;
-  const int KT = a.K >> 5;
-  const int step0 = ks * a.ksteps;
+  const int KT = a.K >> 4;                 // 16-deep k tiles
+  const int step0 = ks * a.ksteps, nsteps = a.ksteps;
 
-  // ---- per-lane load descriptors
   const int arows = max(min(BM, a.M - m0), 0);
   const __amdgpu_buffer_rsrc_t ar =
-      rows_rsrc(a.a + (size_t)m0 * a.lda, arows * a.lda * (int)sizeof(__bf16));
-  int aoff[LA > 0 ? LA : 1];
+      rows_rsrc_sgpr(a.a + (size_t)m0 * a.lda, arows * a.lda * (int)sizeof(__bf16));
+  int aoff[LA];
 #pragma unroll
   for (int i = 0; i < LA; ++i) {
-    const int q = i * 4 + wave, rt = q >> 1, kk = q & 1;
-    aoff[i] = ((rt * 16 + (lane & 15)) * a.lda + kk * 32 + (lane >> 4) * 8) * (int)sizeof(__bf16);
+    const int q = i * 4 + wave, rt = q >> 2, kq = q & 3;   // A fragment q = rt * 4 + kq
+    aoff[i] = ((rt * 32 + (lane & 31)) * a.lda + kq * 16 + (lane >> 5) * 8) * (int)sizeof(__bf16);
   }
-  const __bf16* bptr[LT - LA];
-#pragma unroll
-  for (int i = LA; i < LT; ++i) {
-    const int qb = i * 4 + wave - TA, bt = qb >> 1, kk = qb & 1;
-    const __bf16* w;
-    int ntg;
-    if constexpr (DUAL) {
-      constexpr int NBO = NB / 2;
-      w = bt < NBO ? a.w0 : a.w1;
-      ntg = ntile * NBO + (bt < NBO ? bt : bt - NBO);
-    } else {
-      w = a.w0;
-      ntg = ntile * NB + bt;
-    }
-    bptr[i - LA] = w + ((size_t)ntg * KT + kk) * 512 + lane * 8;
-  }
-
-  bf16x8 pre[LT];
-  auto issue = [&](int step) {
-    const int abase = step * 64 * (int)sizeof(__bf16);
-#pragma unroll
-    for (int i = 0; i < LA; ++i) pre[i] = buf_load8(ar, aoff[i] + abase);
-#pragma unroll
-    for (int i = LA; i < LT; ++i) pre[i] = load8(bptr[i - LA] + (size_t)step * 1024);
-  };
-  auto park = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < LT; ++i) lds[buf * STAGE + (i * 4 + wave) * 64 + lane] = pre[i];
-  };
-
-  // wave's B tiles inside the stage
-  int btw[FN];
+  // this wave's 32-column B tiles: for the gated FFN, FN / 2 gate tiles then FN / 2 up tiles
+  const __bf16* bptr[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
-    if constexpr (DUAL) btw[j] = j < FN / 2 ? wn * (FN / 2) + j : NB / 2 + wn * (FN / 2) + (j - FN / 2);
-    else btw[j] = wn * FN + j;
+    if constexpr (DUAL) {
+      const int half = FN / 2, jj = j < half ? j : j - half;
+      const int ntg = ntile * (BN / 64) + wave * half + jj;
+      bptr[j] = (j < half ? a.w0 : a.w1) + (size_t)ntg * KT * 512 + lane * 8;
+    } else {
+      const int ntg = ntile * (BN / 32) + wave * FN + j;
+      bptr[j] = a.w0 + (size_t)ntg * KT * 512 + lane * 8;
+    }
   }
 
-  f32x4 acc[FM][FN];
+  bf16x8 breg[D][FN][4];
+  auto issue = [&](int s, int slot) {
+    const int st = min(s, nsteps - 1) + step0;   // past the end: a harmless re-load
+    const int abase = st * 64 * (int)sizeof(__bf16);
+#pragma unroll
+    for (int i = 0; i < LA; ++i)
+      buf_load16_lds(ar, &lds[(slot * TA + i * 4 + wave) * 64], aoff[i] + abase);
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int kq = 0; kq < 4; ++kq) breg[slot][j][kq] = load8(bptr[j] + ((size_t)st * 4 + kq) * 512);
+  };
+
+  f32x16 acc[FM][FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = zero4();
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  issue(step0);
-  park(0);
-  __syncthreads();
-  for (int s = 0; s < a.ksteps; ++s) {
-    const bool more = s + 1 < a.ksteps;
-    if (more) issue(step0 + s + 1);
-    const bf16x8* st = lds + (s & 1) * STAGE;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      bf16x8 af[FM], bfr[FN];
+  for (int u = 0; u < D - 1; ++u) issue(u, u);
+
+  for (int s0 = 0; s0 < nsteps; s0 += D) {
 #pragma unroll
-      for (int i = 0; i < FM; ++i) af[i] = st[((wm * FM + i) * 2 + kk) * 64 + lane];
+    for (int u = 0; u < D; ++u) {
+      const int s = s0 + u;
+      __builtin_amdgcn_s_waitcnt(PI0_VMCNT(AWAIT));
+      __builtin_amdgcn_s_barrier();
+      issue(s + D - 1, (u + D - 1) % D);
+      // A fragments through a PF-deep register ring (f = kq * FM + i): the read of
+      // fragment f + PF - 1 is issued before the MFMAs of fragment f.
+      const bf16x8* st = lds + u * TA * 64;
+      bf16x8 ap[PF];
 #pragma unroll
-      for (int j = 0; j < FN; ++j) bfr[j] = st[(TA + btw[j] * 2 + kk) * 64 + lane];
+      for (int p = 0; p < PF - 1; ++p) ap[p] = st[((p % FM) * 4 + p / FM) * 64 + lane];
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+      for (int f = 0; f < 4 * FM; ++f) {
+        const int kq = f / FM, i = f % FM;
+        if (f + PF - 1 < 4 * FM) {
+          const int fn = f + PF - 1;
+          ap[(f + PF - 1) % PF] = st[((fn % FM) * 4 + fn / FM) * 64 + lane];
+        }
+        __builtin_amdgcn_sched_barrier(0);   // keep the prefetch ahead of these MFMAs
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = mfma16(af[i], bfr[j], acc[i][j]);
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(ap[f % PF], breg[u][j][kq], acc[i][j]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    if (more) park((s + 1) & 1);
-    __syncthreads();
   }
+  __builtin_amdgcn_s_waitcnt(PI0_VMCNT(0));   // drain the dummy tail loads before exit
 
-  // ---- epilogue: lane holds C[4g + e][r] of every 16 x 16 fragment
-  const int r = lane & 15, g = lane >> 4;
+  // ---- epilogue: lane holds C[8 (e / 4) + 4 (lane / 32) + e % 4][lane % 32] per fragment
+  const int r = lane & 31, h = lane >> 5;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int row = m0 + wm * (BM / 2) + i * 16 + g * 4 + e;
+    for (int e = 0; e < 16; ++e) {
+      const int row = m0 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
       const bool live = row < a.M;
       if constexpr (EPI == TE_GATE) {
 #pragma unroll
         for (int j = 0; j < FN / 2; ++j) {
-          const int col = (ntile * (NB / 2) + wn * (FN / 2) + j) * 16 + r;
+          const int col = (ntile * (BN / 64) + wave * (FN / 2) + j) * 32 + r;
           const float v = gelu_tanh(acc[i][j][e]) * acc[i][FN / 2 + j][e];
           if (live) a.out[(size_t)row * a.ldo + col] = f2bf(v);
         }
@@ -164,7 +191,7 @@ __global__ __launch_bounds__(256, 1) void tile_gemm_kernel(TileArgs a) {
         const int hd = a.head_dim, qdim = a.heads * hd;
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-          const int col = (ntile * NB + btw[j]) * 16 + r;
+          const int col = (ntile * (BN / 32) + wave * FN + j) * 32 + r;
           const float v = round_bf(acc[i][j][e]);
           const float p = __shfl_xor(v, 1, PI0_WAVE);   // the other column of the RoPE pair
           float o = v;
@@ -184,7 +211,7 @@ __global__ __launch_bounds__(256, 1) void tile_gemm_kernel(TileArgs a) {
       } else {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-          const int col = (ntile * NB + btw[j]) * 16 + r;
+          const int col = (ntile * (BN / 32) + wave * FN + j) * 32 + r;
           float v = acc[i][j][e];
           if (!live) continue;
           if constexpr (EPI == TE_PARTIAL) {
@@ -199,6 +226,28 @@ __global__ __launch_bounds__(256, 1) void tile_gemm_kernel(TileArgs a) {
       }
     }
   }
+}
+
+// W[batch][K][N] -> 32x32x16 B fragments: tile (nt, kt) of 16 k x 32 n is 64 lanes x 8 bf16,
+// lane = (k % 16 / 8) * 32 + n % 32, element k % 8; tiles ordered [nt][kt].
+__global__ void pack_weight32_kernel(const __bf16* __restrict__ w, __bf16* __restrict__ p,
+                                     int K, int N, long long total_frags) {
+  const long long f = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (f >= total_frags) return;
+  const long long per = (long long)(K / 16) * (N / 32) * 64;
+  const long long b = f / per;
+  long long rem = f - b * per;
+  const int lane = (int)(rem & 63);
+  rem >>= 6;
+  const int KT = K / 16;
+  const int kt = (int)(rem % KT), nt = (int)(rem / KT);
+  const int n = nt * 32 + (lane & 31);
+  const int k0 = kt * 16 + (lane >> 5) * 8;
+  const __bf16* src = w + b * (long long)K * N + (long long)k0 * N + n;
+  bf16x8 v;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = src[(long long)j * N];
+  *reinterpret_cast<bf16x8*>(p + f * 8) = v;
 }
 
 // Split-K second pass: sum the partials in split order, add the residual, round once.
@@ -453,20 +502,32 @@ using namespace pi0;
 
 // ---- host-side launch helpers ----------------------------------------------------
 
-template <int BM, int BN, int EPI, bool DUAL>
+template <int BM, int WN, int D, int EPI, bool DUAL, int OCC>
 static int launch_tile(TileArgs a, hipStream_t s) {
   a.tiles_m = (a.M + BM - 1) / BM;
-  const int bn_out = DUAL ? BN / 2 : BN;
+  const int bn_out = DUAL ? 2 * WN : 4 * WN;
   if (a.N % bn_out) return PI0HIP_ERR_SHAPE;
   a.tiles_n = a.N / bn_out;
   const int steps = a.K / 64;
-  if (a.K % 64 || steps % a.splitk) return PI0HIP_ERR_SHAPE;
+  if (a.K % 64 || steps % a.splitk || (steps / a.splitk) % D) return PI0HIP_ERR_SHAPE;
   a.ksteps = steps / a.splitk;
   const int grid = a.tiles_m * a.tiles_n * a.splitk;
   // XCD-contiguous tile order needs a grid divisible by the 8 XCDs
   a.xcd_remap = (grid % 8 == 0) ? 1 : 0;
-  hipLaunchKernelGGL((tile_gemm_kernel<BM, BN, EPI, DUAL>), dim3(grid), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((tile_gemm_kernel<BM, WN, D, EPI, DUAL, OCC>), dim3(grid), dim3(256), 0, s, a);
   return (int)hipGetLastError();
+}
+
+// Pipeline depth: the deepest even ring (<= DMAX) whose depth divides the per-split step count.
+template <int BM, int WN, int DMAX, int EPI, bool DUAL, int OCC = 1>
+static int launch_tile_auto(TileArgs a, hipStream_t s) {
+  if (a.K % 64 || a.splitk < 1 || (a.K / 64) % a.splitk) return PI0HIP_ERR_SHAPE;
+  const int steps = a.K / 64 / a.splitk;
+  if (DMAX >= 8 && steps % 8 == 0) return launch_tile<BM, WN, (DMAX >= 8 ? 8 : 2), EPI, DUAL, OCC>(a, s);
+  if (DMAX >= 6 && steps % 6 == 0) return launch_tile<BM, WN, (DMAX >= 6 ? 6 : 2), EPI, DUAL, OCC>(a, s);
+  if (DMAX >= 4 && steps % 4 == 0) return launch_tile<BM, WN, (DMAX >= 4 ? 4 : 2), EPI, DUAL, OCC>(a, s);
+  if (steps % 2 == 0) return launch_tile<BM, WN, 2, EPI, DUAL, OCC>(a, s);
+  return PI0HIP_ERR_SHAPE;
 }
 
 static TileArgs tile_args(const void* x, int ldx, const void* w, void* out, int ldo, int M, int N,
@@ -481,6 +542,16 @@ static TileArgs tile_args(const void* x, int ldx, const void* w, void* out, int 
 static bool bad_dims(int M, int N, int K) { return M <= 0 || N <= 0 || K <= 0; }
 
 extern "C" {
+
+int pi0hip_pack_weight32(const void* w, void* packed, int K, int N, int batch, hipStream_t s) {
+  if (!w || !packed || K <= 0 || N <= 0 || batch <= 0) return PI0HIP_ERR_ARG;
+  if (K % 16 || N % 32) return PI0HIP_ERR_SHAPE;
+  const long long frags = (long long)batch * (K / 16) * (N / 32) * 64;
+  const long long blocks = (frags + 255) / 256;
+  hipLaunchKernelGGL(pack_weight32_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                     (const __bf16*)w, (__bf16*)packed, K, N, frags);
+  return (int)hipGetLastError();
+}
 
 int pi0hip_rms_norm(const void* x, int ldx, void* out, int ldo, int M, int K, hipStream_t s) {
   if (!x || !out || M <= 0 || K <= 0) return PI0HIP_ERR_ARG;
@@ -503,8 +574,8 @@ int pi0hip_tile_linear(const void* x, int ldx, const void* w_packed, const void*
   if (!x || !w_packed || !out || bad_dims(M, N, K)) return PI0HIP_ERR_ARG;
   TileArgs a = tile_args(x, ldx, w_packed, out, ldo, M, N, K);
   a.bias = (const __bf16*)bias;
-  return bias ? launch_tile<128, 128, TE_BIAS, false>(a, s)
-              : launch_tile<128, 128, TE_STORE, false>(a, s);
+  return bias ? launch_tile_auto<64, 32, 8, TE_BIAS, false>(a, s)
+              : launch_tile_auto<64, 32, 8, TE_STORE, false>(a, s);
 }
 
 int pi0hip_tile_linear_residual(const void* x, int ldx, const void* w_packed, void* out, int ldo,
@@ -513,11 +584,11 @@ int pi0hip_tile_linear_residual(const void* x, int ldx, const void* w_packed, vo
   if (!x || !w_packed || !out || bad_dims(M, N, K) || splitk < 1) return PI0HIP_ERR_ARG;
   TileArgs a = tile_args(x, ldx, w_packed, out, ldo, M, N, K);
   a.splitk = splitk;
-  if (splitk == 1) return launch_tile<64, 128, TE_RES, false>(a, s);
+  if (splitk == 1) return launch_tile_auto<64, 32, 8, TE_RES, false>(a, s);
   if (N % 4 || ldo % 4) return PI0HIP_ERR_SHAPE;
   if (!ws || ws_bytes < pi0hip_tile_workspace_bytes(M, N, splitk)) return PI0HIP_ERR_WORKSPACE;
   a.part = (float*)ws;
-  if (int e = launch_tile<128, 128, TE_PARTIAL, false>(a, s)) return e;
+  if (int e = launch_tile_auto<192, 32, 4, TE_PARTIAL, false>(a, s)) return e;
   hipLaunchKernelGGL(tile_reduce_res_kernel, dim3((M * (N / 4) + 255) / 256), dim3(256), 0, s, a);
   return (int)hipGetLastError();
 }
@@ -527,7 +598,7 @@ int pi0hip_tile_gated_ffn(const void* x, int ldx, const void* gate_packed, const
   if (!x || !gate_packed || !up_packed || !out || bad_dims(M, N, K)) return PI0HIP_ERR_ARG;
   TileArgs a = tile_args(x, ldx, gate_packed, out, ldo, M, N, K);
   a.w1 = (const __bf16*)up_packed;
-  return launch_tile<128, 256, TE_GATE, true>(a, s);
+  return launch_tile_auto<96, 64, 2, TE_GATE, true, 2>(a, s);
 }
 
 int pi0hip_tile_qkv_rope(const void* x, int ldx, const void* w_packed, const void* rope, void* q,
@@ -539,7 +610,7 @@ int pi0hip_tile_qkv_rope(const void* x, int ldx, const void* w_packed, const voi
   TileArgs a = tile_args(x, ldx, w_packed, q, heads * head_dim, M, (heads + 2) * head_dim, K);
   a.out_k = (__bf16*)k; a.out_v = (__bf16*)v; a.ldkv = ldkv;
   a.rope = (const __bf16*)rope; a.heads = heads; a.head_dim = head_dim;
-  return launch_tile<64, 128, TE_QKV_ROPE, false>(a, s);
+  return launch_tile_auto<64, 32, 8, TE_QKV_ROPE, false>(a, s);
 }
 
 int pi0hip_layer_norm(const void* x, int ldx, const void* w, const void* b, void* out, int ldo,

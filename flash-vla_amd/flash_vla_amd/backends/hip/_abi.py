@@ -36,6 +36,7 @@ PROTOTYPES = {
     "pi0hip_attention": (c_int, [P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int, c_int,
                                  c_int, P, c_size_t, P]),
     # prefix encoder
+    "pi0hip_pack_weight32": (c_int, [P, P, c_int, c_int, c_int, P]),
     "pi0hip_rms_norm": (c_int, [P, c_int, P, c_int, c_int, c_int, P]),
     "pi0hip_layer_norm": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_float, P]),
     "pi0hip_tile_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),

@@ -4,8 +4,8 @@ Names and signatures are the reference's `ENCODER_WRAPPERS`
 (`backends/tilelang/wrappers.py:336-401`) plus `encoder_attention`
 (`kernels/attention.py:29-34`, which the reference pipeline calls directly).
 The GEMMs run on the LDS-tiled MFMA kernels of `csrc/pi0_encoder.hip`; the
-weights are read in packed B-fragment order from the shared packed-weight
-cache, like the decoder's.
+weights are read in the 32x32x16 B-fragment order (packed once, layout 32 of the
+shared packed-weight cache).
 """
 from __future__ import annotations
 
@@ -33,7 +33,7 @@ def encoder_projector(x, norm_w, norm_b, proj_w, proj_b, out, x_norm):
         raise ValueError("encoder_projector: shape mismatch")
     _abi.call("pi0hip_layer_norm", _ptr(x2), x2.stride(0), _ptr(norm_w), _ptr(norm_b), _ptr(xn2),
               xn2.stride(0), M, VISION_DIM, LN_EPS, _stream())
-    _abi.call("pi0hip_tile_linear", _ptr(xn2), xn2.stride(0), packed_weight_ptr(proj_w),
+    _abi.call("pi0hip_tile_linear", _ptr(xn2), xn2.stride(0), packed_weight_ptr(proj_w, 32),
               _ptr(proj_b), _ptr(out), out.stride(0), M, N, VISION_DIM, _stream())
     return out
 
@@ -53,7 +53,7 @@ def encoder_norm_qkv_rope(x, weight_qkv, rope, Q, K, V, x_norm):
         raise ValueError("encoder_norm_qkv_rope: shape mismatch")
     _abi.call("pi0hip_rms_norm", _ptr(x), x.stride(0), _ptr(x_norm), x_norm.stride(0), M, Kdim,
               _stream())
-    _abi.call("pi0hip_tile_qkv_rope", _ptr(x_norm), x_norm.stride(0), packed_weight_ptr(weight_qkv),
+    _abi.call("pi0hip_tile_qkv_rope", _ptr(x_norm), x_norm.stride(0), packed_weight_ptr(weight_qkv, 32),
               _ptr(rope), _ptr(Q), _ptr(K), _ptr(V), K.stride(0), M, Kdim, heads, head_dim,
               _stream())
 
@@ -67,7 +67,7 @@ def _tile_residual(x, weight, out, splitk, role):
     lib = _abi.lib()
     nbytes = lib.pi0hip_tile_workspace_bytes(M, N, splitk)
     ws = scratch(f"tile_ws_{role}", (nbytes,), torch.uint8, x.device).data_ptr() if nbytes else None
-    _abi.call("pi0hip_tile_linear_residual", _ptr(x), x.stride(0), packed_weight_ptr(weight),
+    _abi.call("pi0hip_tile_linear_residual", _ptr(x), x.stride(0), packed_weight_ptr(weight, 32),
               _ptr(out), out.stride(0), M, N, K, splitk, ws, nbytes, _stream())
     return out
 
@@ -87,8 +87,8 @@ def encoder_norm_gated_ffn(x, gate_w, up_w, out, x_norm):
         raise ValueError("encoder_norm_gated_ffn: shape mismatch")
     _abi.call("pi0hip_rms_norm", _ptr(x), x.stride(0), _ptr(x_norm), x_norm.stride(0), M, K,
               _stream())
-    _abi.call("pi0hip_tile_gated_ffn", _ptr(x_norm), x_norm.stride(0), packed_weight_ptr(gate_w),
-              packed_weight_ptr(up_w), _ptr(out), out.stride(0), M, N, K, _stream())
+    _abi.call("pi0hip_tile_gated_ffn", _ptr(x_norm), x_norm.stride(0), packed_weight_ptr(gate_w, 32),
+              packed_weight_ptr(up_w, 32), _ptr(out), out.stride(0), M, N, K, _stream())
     return out
 
 

@@ -72,10 +72,10 @@ def _ptr(t: torch.Tensor):
 # and looked up by address on every later call.
 # ---------------------------------------------------------------------------
 class _PackedEntry:
-    __slots__ = ("src", "packed", "base", "nbytes", "K", "N", "version")
+    __slots__ = ("src", "packed", "base", "nbytes", "K", "N", "version", "layout")
 
-    def __init__(self, src, packed, K, N):
-        self.src, self.packed, self.K, self.N = src, packed, K, N
+    def __init__(self, src, packed, K, N, layout):
+        self.src, self.packed, self.K, self.N, self.layout = src, packed, K, N, layout
         self.base = src.data_ptr()
         self.nbytes = src.numel() * src.element_size()
         self.version = src._version
@@ -84,22 +84,28 @@ class _PackedEntry:
 _PACKED: list[_PackedEntry] = []
 
 
-def _pack_into(src: torch.Tensor, dst: torch.Tensor, K: int, N: int) -> None:
+_PACKERS = {16: "pi0hip_pack_weight", 32: "pi0hip_pack_weight32"}
+
+
+def _pack_into(src: torch.Tensor, dst: torch.Tensor, K: int, N: int, layout: int) -> None:
     batch = src.numel() // (K * N)
-    _abi.call("pi0hip_pack_weight", _ptr(src), _ptr(dst), K, N, batch, _stream())
+    _abi.call(_PACKERS[layout], _ptr(src), _ptr(dst), K, N, batch, _stream())
 
 
-def packed_weight_ptr(w: torch.Tensor) -> int:
-    """Device address of the packed copy of `w` ([K, N] bf16, possibly a layer view)."""
+def packed_weight_ptr(w: torch.Tensor, layout: int = 16) -> int:
+    """Device address of the packed copy of `w` ([K, N] bf16, possibly a layer view).
+
+    layout 16: the decoder kernels' 32 k x 16 n fragments (pi0hip_pack_weight);
+    layout 32: the encoder kernels' 16 k x 32 n fragments (pi0hip_pack_weight32)."""
     _check(w, "weight", 2)
     if not w.is_contiguous():
         raise ValueError("weight must be contiguous [K, N]")
     K, N = w.shape
     ptr = w.data_ptr()
     for e in _PACKED:
-        if e.K == K and e.N == N and e.base <= ptr < e.base + e.nbytes:
+        if e.K == K and e.N == N and e.layout == layout and e.base <= ptr < e.base + e.nbytes:
             if not _capturing() and e.version != e.src._version:
-                _pack_into(e.src, e.packed, K, N)
+                _pack_into(e.src, e.packed, K, N, layout)
                 e.version = e.src._version
             return e.packed.data_ptr() + (ptr - e.base)
     if _capturing():
@@ -108,22 +114,24 @@ def packed_weight_ptr(w: torch.Tensor) -> int:
     src = base if (base.dim() >= 2 and base.is_contiguous() and tuple(base.shape[-2:]) == (K, N)
                    and base.dtype == w.dtype) else w
     packed = torch.empty_like(src)
-    _pack_into(src, packed, K, N)
-    entry = _PackedEntry(src, packed, K, N)
+    _pack_into(src, packed, K, N, layout)
+    entry = _PackedEntry(src, packed, K, N, layout)
     _PACKED.append(entry)
     return packed.data_ptr() + (ptr - entry.base)
 
 
 def prepare_weights(weights: dict) -> None:
     """Pack every 2-D/3-D GEMM weight of the decoder and encoder up front (outside any capture)."""
-    for name in ("decoder_action_mlp_w", "decoder_attn_qkv_w", "decoder_attn_o_w",
-                 "decoder_ffn_gate_w", "decoder_ffn_up_w", "decoder_ffn_down_w",
-                 "decoder_action_fused_out_proj_w", "encoder_multi_modal_projector_w",
-                 "encoder_attn_qkv_w", "encoder_attn_o_w", "encoder_ffn_gate_w",
-                 "encoder_ffn_up_w", "encoder_ffn_down_w"):
-        if name in weights:
-            w = weights[name]
-            packed_weight_ptr(w if w.dim() == 2 else w[0])
+    names = {16: ("decoder_action_mlp_w", "decoder_attn_qkv_w", "decoder_attn_o_w",
+                  "decoder_ffn_gate_w", "decoder_ffn_up_w", "decoder_ffn_down_w",
+                  "decoder_action_fused_out_proj_w"),
+             32: ("encoder_multi_modal_projector_w", "encoder_attn_qkv_w", "encoder_attn_o_w",
+                  "encoder_ffn_gate_w", "encoder_ffn_up_w", "encoder_ffn_down_w")}
+    for layout, group in names.items():
+        for name in group:
+            if name in weights:
+                w = weights[name]
+                packed_weight_ptr(w if w.dim() == 2 else w[0], layout)
 
 
 def clear_packed_cache() -> None:

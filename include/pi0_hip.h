@@ -107,8 +107,14 @@ int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int l
                      void* ws, size_t ws_bytes, hipStream_t s);
 
 /* ---- prefix encoder (M = 768..816 token rows, width 2048) --------------------
- * LDS-tiled MFMA GEMMs for the MFMA-bound encoder shapes; weights packed by
- * pi0hip_pack_weight, K % 64 == 0. */
+ * LDS-tiled MFMA GEMMs for the MFMA-bound encoder shapes (32x32x16 MFMAs);
+ * weights packed by pi0hip_pack_weight32, K % 128 == 0. */
+
+/* W[batch][K][N] -> the 32x32x16 B-fragment layout of the encoder GEMMs: tile
+ * (nt, kt) of 16 k x 32 n is 64 lanes x 8 bf16, lane = (k%16/8)*32 + n%32,
+ * element k%8, tiles ordered [nt][kt]. K % 16 == 0, N % 32 == 0. One-time
+ * relayout, like pi0hip_pack_weight (no reference counterpart). */
+int pi0hip_pack_weight32(const void* w, void* packed, int K, int N, int batch, hipStream_t s);
 
 /* out = bf16(x * rsqrt(mean(x^2) + 1e-6)), one row per wave; K in {1024, 2048}.
  * tl_rms_norm, kernels/base.py:373-403 (encoder_norm_qkv_rope / encoder_norm_gated_ffn,
@@ -118,7 +124,7 @@ int pi0hip_rms_norm(const void* x, int ldx, void* out, int ldo, int M, int K, hi
 /* fp32 split-K partials of pi0hip_tile_linear_residual (0 when splitk == 1). */
 size_t pi0hip_tile_workspace_bytes(int M, int N, int splitk);
 
-/* out = x @ W (+ bias[n] when bias != NULL); N % 128 == 0.
+/* out = x @ W (+ bias[n] when bias != NULL); N % 128 == 0, K % 128 == 0.
  * encoder_projector GEMM, wrappers.py:336-344 (tl_matmul_bias, kernels/base.py:158-192) */
 int pi0hip_tile_linear(const void* x, int ldx, const void* w_packed, const void* bias, void* out,
                        int ldo, int M, int N, int K, hipStream_t s);

@@ -59,6 +59,17 @@ def close(got, ref, tol=TOL, what=""):
     assert cos >= 0.99999, f"{what}: cosine {cos}"
 
 
+def test_pack_weight32_layout():
+    """16 k x 32 n fragments: [b][nt][kt][lane][j] = W[b][16 kt + 8 (lane // 32) + j][32 nt + lane % 32]."""
+    w = rnd((2, 64, 64), 10)
+    wd = w.to(DEV)
+    p = torch.empty_like(wd)
+    W._abi.call("pi0hip_pack_weight32", wd.data_ptr(), p.data_ptr(), 64, 64, 2, W._stream())
+    torch.cuda.synchronize()
+    exp = w.reshape(2, 4, 2, 8, 2, 32).permute(0, 4, 1, 2, 5, 3).reshape(-1)
+    assert torch.equal(p.cpu().reshape(-1), exp)
+
+
 @pytest.mark.parametrize("M", [768, 816, 5])
 def test_rms_norm(M):
     x = rnd((M, 2048), 11, 2.0)
