@@ -84,7 +84,11 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
   constexpr int PF = 3;                    // A-fragment register ring
   static_assert(BM % 32 == 0 && WN % 32 == 0 && (!DUAL || WN % 64 == 0), "tile shape");
   static_assert(D >= 2 && AWAIT < 64, "pipeline depth");
-  __shared__ bf16x8 lds[D * TA * 64];
+  constexpr int OUTC = DUAL ? BN / 2 : BN;           // output columns of the block
+  constexpr int CP = OUTC + 4;                       // fp32 pitch of the parked tile
+  constexpr int RING = D * TA * 64;                  // 16-byte slots of the operand ring
+  constexpr int PARK = (BM * CP * 4 + 15) / 16;
+  __shared__ bf16x8 lds[RING > PARK ? RING : PARK];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   int id = blockIdx.x;
@@ -172,59 +176,81 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
   }
   __builtin_amdgcn_s_waitcnt(PI0_VMCNT(0));   // drain the dummy tail loads before exit
 
-  // ---- epilogue: lane holds C[8 (e / 4) + 4 (lane / 32) + e % 4][lane % 32] per fragment
-  const int r = lane & 31, h = lane >> 5;
+  // ---- epilogue through LDS (the ring is free now): the waves park their fp32 tiles
+  // row-major, then every thread finishes 8 consecutive output columns of a row with
+  // 16-byte loads and stores (residual, RoPE table, outputs, split-K partials).
+  // Lane holds C[8 (e / 4) + 4 (lane / 32) + e % 4][lane % 32] of each fragment.
+  __syncthreads();
+  float* cs = reinterpret_cast<float*>(lds);
+  {
+    const int r = lane & 31, h = lane >> 5;
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int row = m0 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-      const bool live = row < a.M;
-      if constexpr (EPI == TE_GATE) {
+      for (int e = 0; e < 16; ++e) {
+        const int row = i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+        if constexpr (DUAL) {
 #pragma unroll
-        for (int j = 0; j < FN / 2; ++j) {
-          const int col = (ntile * (BN / 64) + wave * (FN / 2) + j) * 32 + r;
-          const float v = gelu_tanh(acc[i][j][e]) * acc[i][FN / 2 + j][e];
-          if (live) a.out[(size_t)row * a.ldo + col] = f2bf(v);
-        }
-      } else if constexpr (EPI == TE_QKV_ROPE) {
-        const int hd = a.head_dim, qdim = a.heads * hd;
+          for (int j = 0; j < FN / 2; ++j)
+            cs[row * CP + (wave * (FN / 2) + j) * 32 + r] =
+                gelu_tanh(acc[i][j][e]) * acc[i][FN / 2 + j][e];
+        } else {
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int col = (ntile * (BN / 32) + wave * FN + j) * 32 + r;
-          const float v = round_bf(acc[i][j][e]);
-          const float p = __shfl_xor(v, 1, PI0_WAVE);   // the other column of the RoPE pair
-          float o = v;
-          if (col < qdim + hd && live) {
-            const __bf16* rp = a.rope + (size_t)row * hd + ((col % hd) & ~1);
-            const float cs = bf2f(rp[0]), sn = bf2f(rp[1]);
-            o = (col & 1) ? v * cs + p * sn : v * cs - p * sn;
-          }
-          if (live) {
-            __bf16* dst;
-            if (col < qdim) dst = a.out + (size_t)row * qdim + col;
-            else if (col < qdim + hd) dst = a.out_k + (size_t)row * a.ldkv + (col - qdim);
-            else dst = a.out_v + (size_t)row * a.ldkv + (col - qdim - hd);
-            *dst = f2bf(o);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const int col = (ntile * (BN / 32) + wave * FN + j) * 32 + r;
-          float v = acc[i][j][e];
-          if (!live) continue;
-          if constexpr (EPI == TE_PARTIAL) {
-            a.part[((size_t)ks * a.M + row) * a.N + col] = v;
-            continue;
-          }
-          __bf16* dst = a.out + (size_t)row * a.ldo + col;
-          if constexpr (EPI == TE_BIAS) v += bf2f(a.bias[col]);
-          if constexpr (EPI == TE_RES) v += bf2f(*dst);
-          *dst = f2bf(v);
+          for (int j = 0; j < FN; ++j) cs[row * CP + (wave * FN + j) * 32 + r] = acc[i][j][e];
         }
       }
+  }
+  __syncthreads();
+  constexpr int C8 = OUTC / 8;
+  for (int idx = t; idx < BM * C8; idx += 256) {
+    const int row = idx / C8, c = (idx - row * C8) * 8;
+    const int grow = m0 + row;
+    if (grow >= a.M) continue;
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(&cs[row * CP + c]);
+    const f32x4 hi = *reinterpret_cast<const f32x4*>(&cs[row * CP + c + 4]);
+    float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    const int col = ntile * OUTC + c;
+    if constexpr (EPI == TE_PARTIAL) {
+      float* dst = a.part + ((size_t)ks * a.M + grow) * a.N + col;
+      *reinterpret_cast<f32x4*>(dst) = lo;
+      *reinterpret_cast<f32x4*>(dst + 4) = hi;
+      continue;
     }
+    __bf16* dst;
+    if constexpr (EPI == TE_QKV_ROPE) {
+      const int hd = a.head_dim, qdim = a.heads * hd;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = round_bf(v[q]);
+      if (col < qdim + hd) {          // rotate the rounded pairs (2p, 2p + 1)
+        const bf16x8 rp = load8(a.rope + (size_t)grow * hd + (col % hd));
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const float cs_ = bf2f(rp[2 * p]), sn = bf2f(rp[2 * p + 1]);
+          const float x0 = v[2 * p], x1 = v[2 * p + 1];
+          v[2 * p] = x0 * cs_ - x1 * sn;
+          v[2 * p + 1] = x1 * cs_ + x0 * sn;
+        }
+      }
+      if (col < qdim) dst = a.out + (size_t)grow * qdim + col;
+      else if (col < qdim + hd) dst = a.out_k + (size_t)grow * a.ldkv + (col - qdim);
+      else dst = a.out_v + (size_t)grow * a.ldkv + (col - qdim - hd);
+    } else {
+      dst = a.out + (size_t)grow * a.ldo + col;
+      if constexpr (EPI == TE_BIAS) {
+        const bf16x8 b = load8(a.bias + col);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] += bf2f(b[q]);
+      }
+      if constexpr (EPI == TE_RES) {
+        const bf16x8 rv = load8(dst);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] += bf2f(rv[q]);
+      }
+    }
+    bf16x8 o;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) o[q] = f2bf(v[q]);
+    *reinterpret_cast<bf16x8*>(dst) = o;
   }
 }
 
@@ -337,163 +363,185 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const __bf16* __restric
 
 // ---- encoder multi-query attention (attention.py:29-34): every flat query row
 // (token * heads + head) attends over all keys of the one KV head, no mask.
-// Workgroup = 32 query rows; wave w takes row tile w & 1 and key half w >> 1 of
-// each 64-key block. K / V blocks are staged through LDS; per wave an online
-// (flash) softmax in the log2 domain with S^T = K Q^T, so the probabilities are
-// already the A operand of P @ V (same key-slot permutation as the decoder
-// kernel). The logits are rounded to bf16 as the reference's bf16 matmul does.
+//
+// Workgroup = 32 query rows; wave w takes the 32-key blocks b with b % 4 == w, so
+// each K / V byte is read once per workgroup, straight from L2 into registers
+// (no LDS staging, no barriers in the key loop). Per block, with 32x32x16 MFMAs:
+//   S^T[32 keys][32 q] = K Q^T      A = K rows (16 B loads), B = Q^T (held all along)
+//   online softmax per query in the log2 domain (the logits are rounded to bf16
+//   first, as the reference's bf16 matmul output is); each lane owns one query
+//   and 16 of its keys, the other 16 sit in lane ^ 32;
+//   O^T[256 d][32 q] += V^T P^T     A = V^T (rows of the transposed V, pre-pass
+//   below), B = P^T, which is exactly the S^T accumulator's layout once the key
+//   slots of V^T are permuted the same way -- P never moves between lanes and
+//   the per-query rescale is lane-local.
+// The 4 waves' partial (m, l, O^T) are merged through LDS at the end.
 constexpr int EA_HD = 256;
-constexpr int EA_KB = 64;                 // keys per block (32 per key half)
-constexpr int EA_P = EA_HD + 8;           // bf16 pitch of staged rows
-constexpr int EA_OP = EA_HD + 4;          // fp32 pitch of the merge buffer
 
 struct EncAttnArgs {
   const __bf16* q; int ldq;
-  const __bf16* k; const __bf16* v; int ldkv;
+  const __bf16* k; int ldk;
+  const __bf16* vt; int ldvt;           // V^T [256][ldvt], keys zero-padded to a multiple of 32
   __bf16* out; int ldo;
   int rows, keys;
   float scale_log2;
 };
 
+// V [keys][ldv] -> V^T [256][ldvt], zero beyond `keys` (64 x 64 tiles through LDS).
+// Inside every 16-key chunk the keys are stored in the order the P^T operand uses,
+// {0-3, 8-11, 4-7, 12-15}, so one lane's 8 keys are one 16-byte load.
+__global__ __launch_bounds__(256) void transpose_v_kernel(const __bf16* __restrict__ v, int ldv,
+                                                          __bf16* __restrict__ vt, int ldvt,
+                                                          int keys) {
+  __shared__ __bf16 tile[64][66];
+  const int k0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
+  const int t = threadIdx.x;
+  for (int i = t; i < 64 * 64; i += 256) {
+    const int kr = i >> 6, dc = i & 63;
+    tile[kr][dc] = (k0 + kr < keys) ? v[(size_t)(k0 + kr) * ldv + d0 + dc] : __bf16(0.f);
+  }
+  __syncthreads();
+  for (int i = t; i < 64 * 64; i += 256) {
+    const int dr = i >> 6, kc = i & 63;      // kc = storage slot; its key:
+    const int sl = kc & 15, key = (kc & ~15) + ((sl & 4) ? 8 : 0) + ((sl & 8) ? 4 : 0) + (sl & 3);
+    vt[(size_t)(d0 + dr) * ldvt + k0 + kc] = tile[key][dr];
+  }
+}
+
 __global__ __launch_bounds__(256, 1) void enc_attn_kernel(EncAttnArgs a) {
-  __shared__ __attribute__((aligned(16))) __bf16 ks_[EA_KB][EA_P];   // also the merge buffer
-  __shared__ __attribute__((aligned(16))) __bf16 vs_[EA_KB][EA_P];
-  __shared__ float mrg_m[2][16], mrg_l[2][16];   // [row tile][row] of key half 1
+  constexpr int OP = 33;                               // fp32 pitch of the parked O^T columns
+  __shared__ float ob[3][EA_HD][OP];                   // waves 1..3: O^T[d][q]; first Q^T
+  __shared__ float ml[4][2][32];                       // per wave: m and l of each query
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int r = lane & 15, g = lane >> 4;
-  const int rt = wave & 1, half = wave >> 1;
-  const int q0 = blockIdx.x * 32 + rt * 16;
+  const int r = lane & 31, h = lane >> 5;
+  const int q0 = blockIdx.x * 32;
 
-  // Q^T fragments of this wave's 16 rows (B operand), straight from global memory
-  bf16x8 qf[8];
+  // Q^T fragments (B operand, 16 d each; lane holds Q[q0 + r][16 kk + 8 h .. + 7]) are
+  // shared by the 4 waves: staged once in LDS (in the merge buffer's space)
+  bf16x8* qs = reinterpret_cast<bf16x8*>(&ob[0][0][0]);    // [16 kk][64 lanes]
   {
     const __amdgpu_buffer_rsrc_t qr =
-        rows_rsrc(a.q + (size_t)q0 * a.ldq, max(min(16, a.rows - q0), 0) * a.ldq * 2);
+        rows_rsrc(a.q + (size_t)q0 * a.ldq, max(min(32, a.rows - q0), 0) * a.ldq * 2);
 #pragma unroll
-    for (int kq = 0; kq < 8; ++kq) qf[kq] = buf_load8(qr, (r * a.ldq + kq * 32 + g * 8) * 2);
+    for (int i = 0; i < 4; ++i) {
+      const int kk = wave * 4 + i;
+      qs[kk * 64 + lane] = buf_load8(qr, (r * a.ldq + kk * 16 + h * 8) * 2);
+    }
   }
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t kr = rows_rsrc(a.k, a.keys * a.ldk * 2);
 
-  const __amdgpu_buffer_rsrc_t kr = rows_rsrc(a.k, a.keys * a.ldkv * 2);
-  const __amdgpu_buffer_rsrc_t vr = rows_rsrc(a.v, a.keys * a.ldkv * 2);
-  const int srow = t >> 5, sch = t & 31;     // staging: 8 rows x 32 chunks per pass
-  bf16x8 kv[8], vv[8];
-  auto issue = [&](int kb) {
-    const int off = ((kb * EA_KB + srow) * a.ldkv + sch * 8) * 2;
-    const int step = 8 * a.ldkv * 2;
+  float m_run = -1.0e30f, l_run = 0.f;
+  f32x16 o[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) kv[j] = buf_load8(kr, off + j * step);
+  for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) vv[j] = buf_load8(vr, off + j * step);
+    for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+
+  const int nblk = (a.keys + 31) / 32;
+  const int mine = nblk > wave ? (nblk - wave + 3) / 4 : 0;     // blocks b = wave + 4 i
+  // Staggered single buffers: V^T of block i is requested before its S^T MFMAs, and
+  // K of block i + 1 right after them (into the registers they just consumed), so
+  // each load has the other phase's 16 MFMAs to land.
+  bf16x8 kf[16], vf[8][2];
+  auto blk = [&](int i) { return wave + 4 * min(i, mine - 1); };   // past the end: re-load
+  auto load_k = [&](int i) {
+    const int key0 = blk(i) * 32;
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk)
+      kf[kk] = buf_load8(kr, ((key0 + r) * a.ldk + kk * 16 + h * 8) * 2);
   };
-
-  float m_run = -1.0e30f, l_run = 0.f;     // per query row r (replicated over g)
-  f32x4 o[16];
+  auto load_v = [&](int i) {
+    const int key0 = blk(i) * 32;
 #pragma unroll
-  for (int dt = 0; dt < 16; ++dt) o[dt] = zero4();
-
-  const int nblk = (a.keys + EA_KB - 1) / EA_KB;
-  issue(0);
-  for (int kb = 0; kb < nblk; ++kb) {
-    __syncthreads();                           // previous block fully consumed
+    for (int dt = 0; dt < 8; ++dt) {
+      const __bf16* row = a.vt + (size_t)(dt * 32 + r) * a.ldvt + key0 + 8 * h;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      *reinterpret_cast<bf16x8*>(&ks_[srow + 8 * j][sch * 8]) = kv[j];
-      *reinterpret_cast<bf16x8*>(&vs_[srow + 8 * j][sch * 8]) = vv[j];
+      for (int c = 0; c < 2; ++c) vf[dt][c] = load8(row + 16 * c);
     }
-    __syncthreads();
-    if (kb + 1 < nblk) issue(kb + 1);
-
-    const int kw = half * 32;
-    f32x4 st[2] = {zero4(), zero4()};
+  };
+  if (mine > 0) load_k(0);
+  for (int i = 0; i < mine; ++i) {
+    const int key0 = (wave + 4 * i) * 32;
+    load_v(i);
+    f32x16 st;
 #pragma unroll
-    for (int kq = 0; kq < 8; ++kq) {
-      const bf16x8 k0f = *reinterpret_cast<const bf16x8*>(&ks_[kw + r][kq * 32 + g * 8]);
-      const bf16x8 k1f = *reinterpret_cast<const bf16x8*>(&ks_[kw + 16 + r][kq * 32 + g * 8]);
-      st[0] = mfma16(k0f, qf[kq], st[0]);
-      st[1] = mfma16(k1f, qf[kq], st[1]);
+    for (int e = 0; e < 16; ++e) st[e] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) st = mfma32(kf[kk], qs[kk * 64 + lane], st);
+    load_k(i + 1);
+    // lane holds S^T[key 8 (e / 4) + 4 h + e % 4][query r]
+    float sv[16], mx = -1.0e30f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int key = key0 + 8 * (e >> 2) + 4 * h + (e & 3);
+      sv[e] = key < a.keys ? round_bf(st[e]) * a.scale_log2 : -1.0e30f;
+      mx = fmaxf(mx, sv[e]);
     }
-    float s[8], mx = -1.0e30f;
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int key = kb * EA_KB + kw + nt * 16 + g * 4 + e;
-        const float v = key < a.keys ? round_bf(st[nt][e]) * a.scale_log2 : -1.0e30f;
-        s[nt * 4 + e] = v;
-        mx = fmaxf(mx, v);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, PI0_WAVE));
     mx = fmaxf(mx, __shfl_xor(mx, 32, PI0_WAVE));
     const float m_new = fmaxf(m_run, mx);
     const float alpha = fast_exp2(m_run - m_new);
     float ps = 0.f;
-    bf16x8 pf;
+    bf16x8 pf[2];                                      // P^T for chunk c = e / 8
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float p = fast_exp2(s[j] - m_new);
-      ps += p;
-      pf[j] = f2bf(p);
+    for (int e = 0; e < 16; ++e) {
+      const float pv = fast_exp2(sv[e] - m_new);
+      ps += pv;
+      pf[e >> 3][e & 7] = f2bf(pv);
     }
-    ps += __shfl_xor(ps, 16, PI0_WAVE);
     ps += __shfl_xor(ps, 32, PI0_WAVE);
     l_run = l_run * alpha + ps;
     m_run = m_new;
-    // O rows are 4g + e: fetch those rows' rescale factors
-    float al[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) al[e] = __shfl(alpha, g * 4 + e, PI0_WAVE);
+    for (int dt = 0; dt < 8; ++dt) {
+      f32x16 acc = o[dt] * alpha;
 #pragma unroll
-    for (int dt = 0; dt < 16; ++dt) {
-      const int col = dt * 16 + r;
-      bf16x8 vf;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        vf[j] = vs_[kw + g * 4 + j][col];
-        vf[4 + j] = vs_[kw + 16 + g * 4 + j][col];
-      }
-      f32x4 sc;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sc[e] = o[dt][e] * al[e];
-      o[dt] = mfma16(pf, vf, sc);
+      for (int c = 0; c < 2; ++c) acc = mfma32(vf[dt][c], pf[c], acc);
+      o[dt] = acc;
     }
   }
+  __syncthreads();                                     // every wave is done with qs
 
-  // ---- merge the two key halves of each row tile through LDS
-  __syncthreads();
-  if (half == 1 && g == 0) { mrg_m[rt][r] = m_run; mrg_l[rt][r] = l_run; }
-  float* ob = reinterpret_cast<float*>(&ks_[0][0]);     // [2 row tiles][16][EA_OP], half 1 only
-  if (half == 1) {
+  // ---- merge the 4 waves' partials: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w
+  if (h == 0) { ml[wave][0][r] = m_run; ml[wave][1][r] = l_run; }
+  if (wave > 0) {
 #pragma unroll
-    for (int dt = 0; dt < 16; ++dt)
+    for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) ob[(rt * 16 + g * 4 + e) * EA_OP + dt * 16 + r] = o[dt][e];
+      for (int e = 0; e < 16; ++e)
+        ob[wave - 1][dt * 32 + 8 * (e >> 2) + 4 * h + (e & 3)][r] = o[dt][e];
   }
   __syncthreads();
-  if (half == 1) return;
-  // wave rt (key half 0) merges with wave rt + 2 (key half 1) of the same row tile
-  float w0[4], w1[4];
+  if (wave > 0) return;
+  float M = -1.0e30f;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int rr = g * 4 + e;
-    const float ma = __shfl(m_run, rr, PI0_WAVE), la = __shfl(l_run, rr, PI0_WAVE);
-    const float mb = mrg_m[rt][rr], lb = mrg_l[rt][rr];
-    const float M = fmaxf(ma, mb);
-    const float ea = fast_exp2(ma - M), eb = fast_exp2(mb - M);
-    const float inv = __builtin_amdgcn_rcpf(la * ea + lb * eb);
-    w0[e] = ea * inv;
-    w1[e] = eb * inv;
+  for (int w = 0; w < 4; ++w) M = fmaxf(M, ml[w][0][r]);
+  float wgt[4], L = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    wgt[w] = fast_exp2(ml[w][0][r] - M);     // 0 for a wave that saw no key
+    L += wgt[w] * ml[w][1][r];
   }
+  const float inv = __builtin_amdgcn_rcpf(L);
+  const int row = q0 + r;
+  if (row >= a.rows) return;
+  __bf16* orow = a.out + (size_t)row * a.ldo;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int row = q0 + g * 4 + e;
-    if (row >= a.rows) continue;
+  for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < 16; ++dt) {
-      const float v = o[dt][e] * w0[e] + ob[(rt * 16 + g * 4 + e) * EA_OP + dt * 16 + r] * w1[e];
-      a.out[(size_t)row * a.ldo + dt * 16 + r] = f2bf(v);
+    for (int e4 = 0; e4 < 4; ++e4) {           // 4 consecutive d per store
+      bf16x4 pk;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = dt * 32 + 8 * e4 + 4 * h + e;
+        float v = o[dt][e4 * 4 + e] * wgt[0];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) v += ob[w - 1][d][r] * wgt[w];
+        pk[e] = f2bf(v * inv);
+      }
+      *reinterpret_cast<bf16x4*>(orow + dt * 32 + 8 * e4 + 4 * h) = pk;
     }
-  }
 }
 
 }  // namespace pi0
@@ -540,6 +588,11 @@ static TileArgs tile_args(const void* x, int ldx, const void* w, void* out, int 
 }
 
 static bool bad_dims(int M, int N, int K) { return M <= 0 || N <= 0 || K <= 0; }
+// 16-byte vector access in the staging loads and the epilogues: row starts must be
+// 16-byte aligned (leading dimension a multiple of 8 bf16, pointer 16-byte aligned).
+static bool misaligned(const void* p, int ld) {
+  return (reinterpret_cast<uintptr_t>(p) & 15) != 0 || (ld & 7) != 0;
+}
 
 extern "C" {
 
@@ -572,6 +625,7 @@ size_t pi0hip_tile_workspace_bytes(int M, int N, int splitk) {
 int pi0hip_tile_linear(const void* x, int ldx, const void* w_packed, const void* bias, void* out,
                        int ldo, int M, int N, int K, hipStream_t s) {
   if (!x || !w_packed || !out || bad_dims(M, N, K)) return PI0HIP_ERR_ARG;
+  if (misaligned(x, ldx) || misaligned(out, ldo) || misaligned(bias, 0)) return PI0HIP_ERR_SHAPE;
   TileArgs a = tile_args(x, ldx, w_packed, out, ldo, M, N, K);
   a.bias = (const __bf16*)bias;
   return bias ? launch_tile_auto<64, 32, 8, TE_BIAS, false>(a, s)
@@ -582,6 +636,7 @@ int pi0hip_tile_linear_residual(const void* x, int ldx, const void* w_packed, vo
                                 int M, int N, int K, int splitk, void* ws, size_t ws_bytes,
                                 hipStream_t s) {
   if (!x || !w_packed || !out || bad_dims(M, N, K) || splitk < 1) return PI0HIP_ERR_ARG;
+  if (misaligned(x, ldx) || misaligned(out, ldo)) return PI0HIP_ERR_SHAPE;
   TileArgs a = tile_args(x, ldx, w_packed, out, ldo, M, N, K);
   a.splitk = splitk;
   if (splitk == 1) return launch_tile_auto<64, 32, 8, TE_RES, false>(a, s);
@@ -596,6 +651,7 @@ int pi0hip_tile_linear_residual(const void* x, int ldx, const void* w_packed, vo
 int pi0hip_tile_gated_ffn(const void* x, int ldx, const void* gate_packed, const void* up_packed,
                           void* out, int ldo, int M, int N, int K, hipStream_t s) {
   if (!x || !gate_packed || !up_packed || !out || bad_dims(M, N, K)) return PI0HIP_ERR_ARG;
+  if (misaligned(x, ldx) || misaligned(out, ldo)) return PI0HIP_ERR_SHAPE;
   TileArgs a = tile_args(x, ldx, gate_packed, out, ldo, M, N, K);
   a.w1 = (const __bf16*)up_packed;
   return launch_tile_auto<96, 64, 2, TE_GATE, true, 2>(a, s);
@@ -606,7 +662,9 @@ int pi0hip_tile_qkv_rope(const void* x, int ldx, const void* w_packed, const voi
                          hipStream_t s) {
   if (!x || !w_packed || !rope || !q || !k || !v || M <= 0 || K <= 0 || heads <= 0)
     return PI0HIP_ERR_ARG;
-  if (head_dim % 16) return PI0HIP_ERR_SHAPE;
+  if (head_dim % 16 || misaligned(x, ldx) || misaligned(q, 0) || misaligned(k, ldkv) ||
+      misaligned(v, ldkv) || misaligned(rope, head_dim))
+    return PI0HIP_ERR_SHAPE;
   TileArgs a = tile_args(x, ldx, w_packed, q, heads * head_dim, M, (heads + 2) * head_dim, K);
   a.out_k = (__bf16*)k; a.out_v = (__bf16*)v; a.ldkv = ldkv;
   a.rope = (const __bf16*)rope; a.heads = heads; a.head_dim = head_dim;
@@ -622,14 +680,30 @@ int pi0hip_layer_norm(const void* x, int ldx, const void* w, const void* b, void
   return (int)hipGetLastError();
 }
 
+static inline size_t round256_(size_t v) { return (v + 255) / 256 * 256; }
+
+size_t pi0hip_encoder_attention_workspace_bytes(int keys) {
+  if (keys <= 0) return 0;
+  const size_t ldvt = (size_t)(keys + 63) / 64 * 64;
+  return round256_((size_t)EA_HD * ldvt * sizeof(__bf16));
+}
+
 int pi0hip_encoder_attention(const void* q, int ldq, const void* k, const void* v, int ldkv,
                              void* out, int ldo, int rows, int keys, int head_dim, float scale,
-                             hipStream_t s) {
+                             void* ws, size_t ws_bytes, hipStream_t s) {
   if (!q || !k || !v || !out || rows <= 0 || keys <= 0) return PI0HIP_ERR_ARG;
-  if (head_dim != EA_HD) return PI0HIP_ERR_SHAPE;
+  if (head_dim != EA_HD || misaligned(q, ldq) || misaligned(k, ldkv) || (ldo & 3) ||
+      (reinterpret_cast<uintptr_t>(out) & 7))
+    return PI0HIP_ERR_SHAPE;
+  if (!ws || ws_bytes < pi0hip_encoder_attention_workspace_bytes(keys)) return PI0HIP_ERR_WORKSPACE;
+  const int ldvt = (keys + 63) / 64 * 64;
+  hipLaunchKernelGGL(transpose_v_kernel, dim3(ldvt / 64, EA_HD / 64), dim3(256), 0, s,
+                     (const __bf16*)v, ldkv, (__bf16*)ws, ldvt, keys);
+  if (hipError_t e = hipGetLastError()) return (int)e;
   EncAttnArgs a = {};
   a.q = (const __bf16*)q; a.ldq = ldq;
-  a.k = (const __bf16*)k; a.v = (const __bf16*)v; a.ldkv = ldkv;
+  a.k = (const __bf16*)k; a.ldk = ldkv;
+  a.vt = (const __bf16*)ws; a.ldvt = ldvt;
   a.out = (__bf16*)out; a.ldo = ldo;
   a.rows = rows; a.keys = keys;
   a.scale_log2 = 1.4426950408889634f * scale;

@@ -46,8 +46,9 @@ PROTOTYPES = {
     "pi0hip_tile_gated_ffn": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, P]),
     "pi0hip_tile_qkv_rope": (c_int, [P, c_int, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int,
                                      P]),
+    "pi0hip_encoder_attention_workspace_bytes": (c_size_t, [c_int]),
     "pi0hip_encoder_attention": (c_int, [P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int,
-                                         c_float, P]),
+                                         c_float, P, c_size_t, P]),
 }
 
 ERRORS = {-1: "invalid argument", -2: "unsupported shape", -3: "workspace missing or too small"}

@@ -108,8 +108,11 @@ def encoder_attention(Q, K, V, scale):
     if V.shape != K.shape or K.shape[1] != head_dim or K.stride(0) != V.stride(0):
         raise ValueError("encoder_attention: shape mismatch")
     out = scratch("encoder_attn_out", (rows, head_dim), Q.dtype, Q.device)
+    nbytes = _abi.lib().pi0hip_encoder_attention_workspace_bytes(keys)
+    ws = scratch("encoder_attn_ws", (nbytes,), torch.uint8, Q.device)
     _abi.call("pi0hip_encoder_attention", _ptr(Q), Q.stride(0), _ptr(K), _ptr(V), K.stride(0),
-              _ptr(out), out.stride(0), rows, keys, head_dim, float(scale), _stream())
+              _ptr(out), out.stride(0), rows, keys, head_dim, float(scale), ws.data_ptr(), nbytes,
+              _stream())
     width = 2048 if (rows * head_dim) % 2048 == 0 else head_dim
     return out.view(-1, width)
 

@@ -197,7 +197,7 @@ ENCODER_WEIGHT_NAMES = ("encoder_attn_qkv_w", "encoder_attn_o_w", "encoder_ffn_g
 def encoder_checkpoint(seed: int = 2, std: float = 0.02, layers: int = ENCODER_LAYERS,
                        width: int = ENCODER_WIDTH, ffn: int = ENCODER_FFN,
                        heads: int = DECODER_HEADS, head_dim: int = HEAD_DIM,
-                       device: str = "cpu") -> dict:
+                       device: str = "cpu", draw_on_device: bool = False) -> dict:
     """Packed prefix-encoder tensors, N(0, std) per element.
 
     With Gemma RMSNorm weights 0 the fold of `fold_decoder` multiplies the
@@ -206,9 +206,10 @@ def encoder_checkpoint(seed: int = 2, std: float = 0.02, layers: int = ENCODER_L
     distribution (the fold algebra itself is pinned against the unfolded layer
     at small size by the oracle tests). Drawn layer by layer on the CPU
     generator, rounded to bf16 at once, so the 18-layer set (~4 GB) never exists
-    in fp32.
+    in fp32. `draw_on_device=True` draws on `device`'s own seeded generator
+    instead (fast; the values then differ from the CPU draw).
     """
-    gen = _gen(seed)
+    gen = (torch.Generator(device=device).manual_seed(seed) if draw_on_device else _gen(seed))
     shapes = {
         "encoder_attn_qkv_w": (width, (heads + 2) * head_dim),
         "encoder_attn_o_w": (heads * head_dim, width),
@@ -220,7 +221,8 @@ def encoder_checkpoint(seed: int = 2, std: float = 0.02, layers: int = ENCODER_L
            for n, sh in shapes.items()}
     for i in range(layers):
         for n, sh in shapes.items():
-            out[n][i].copy_((torch.randn(sh, generator=gen) * std).to(torch.bfloat16))
+            draw = torch.randn(sh, generator=gen, device=gen.device)
+            out[n][i].copy_((draw * std).to(torch.bfloat16))
     return out
 
 

@@ -108,7 +108,8 @@ int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int l
 
 /* ---- prefix encoder (M = 768..816 token rows, width 2048) --------------------
  * LDS-tiled MFMA GEMMs for the MFMA-bound encoder shapes (32x32x16 MFMAs);
- * weights packed by pi0hip_pack_weight32, K % 128 == 0. */
+ * weights packed by pi0hip_pack_weight32, K % 128 == 0; activation / output rows
+ * 16-byte aligned (pointers 16-byte aligned, leading dimensions % 8 == 0). */
 
 /* W[batch][K][N] -> the 32x32x16 B-fragment layout of the encoder GEMMs: tile
  * (nt, kt) of 16 k x 32 n is 64 lanes x 8 bf16, lane = (k%16/8)*32 + n%32,
@@ -158,12 +159,16 @@ int pi0hip_tile_qkv_rope(const void* x, int ldx, const void* w_packed, const voi
 int pi0hip_layer_norm(const void* x, int ldx, const void* w, const void* b, void* out, int ldo,
                       int M, int K, float eps, hipStream_t s);
 
+/* Workspace of pi0hip_encoder_attention: the transposed V (256 x keys rounded up to 64). */
+size_t pi0hip_encoder_attention_workspace_bytes(int keys);
+
 /* out = softmax(scale * bf16(q k^T)) v, every flat query row over every key
  * (one shared KV head, no mask); head_dim must be 256. `out` must not alias q.
+ * Two launches: V -> V^T into the workspace, then the attention.
  * encoder_attention, kernels/attention.py:29-34 */
 int pi0hip_encoder_attention(const void* q, int ldq, const void* k, const void* v, int ldkv,
                              void* out, int ldo, int rows, int keys, int head_dim, float scale,
-                             hipStream_t s);
+                             void* ws, size_t ws_bytes, hipStream_t s);
 
 #ifdef __cplusplus
 }
