@@ -38,9 +38,10 @@ KV_WRITE_BYTES = LAYERS * 51 * 256 * 2 * 2
 STEP_BYTES = LAYERS * LAYER_WEIGHT_BYTES + SMALL_PROJ_BYTES + KV_READ_BYTES + KV_WRITE_BYTES
 CHUNK_BYTES = STEPS * STEP_BYTES           # 6,411,223,680 B
 GATE_BYTES = 2 * 1024 * 4096 * 2           # gate + up weights of one layer (activations excluded)
-# HBM bytes per launch of the gate kernel from rocprofv3 FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0
-# (factors from a plain 256 MiB copy); profiles/decoder_kernels_config2_hbm_traffic.md
-GATE_TRAFFIC_BYTES = (8685.5 * 2.0 + 408.0 * 1.0) * 1024
+# HBM bytes per launch from rocprofv3 FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (KiB; factors from a
+# plain 256 MiB copy); profiles/kernels_hbm_traffic_config2_config3.md
+GATE_TRAFFIC_BYTES = (8661.5 * 2.0 + 408.0 * 1.0) * 1024
+ENC_GATE_TRAFFIC_BYTES = (111737.9 * 2.0 + 24576.0 * 1.0) * 1024
 
 
 def _time_graph(run, n_inner, reps, torch):
@@ -182,7 +183,7 @@ def main_encoder(args, torch):
         roof = {"kernel": "tile_gemm_kernel<TE_GATE> + rms_norm_kernel (encoder_norm_gated_ffn)",
                 "bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-                "traffic": None, "avg_launch_us": round(us, 3), "flops_per_launch": gate_flops}
+                "traffic": int(ENC_GATE_TRAFFIC_BYTES), "avg_launch_us": round(us, 3), "flops_per_launch": gate_flops}
     cpu = None
     if not args.no_cpu:
         ck_cpu = encoder_checkpoint(seed=2, layers=2)
