@@ -2,7 +2,8 @@
 
 `--workload encoder` measures the prefix encoder instead:
 ms per encode of M = 768 rows through 18 layers, with the gated-FFN GEMM's
-MFMA roofline and the CPU oracle on a one-layer sample.
+MFMA roofline and the CPU oracle on a one-layer sample. `--workload full`
+times the whole one-graph forward (config 4) against the published H100 figure.
 
 One "step" of this benchmark = one replay of the captured decoder loop: 10
 Euler steps x 18 layers at M = 51 rows against 819 keys,
@@ -207,13 +208,61 @@ def main_encoder(args, torch):
     print(json.dumps(out), flush=True)
 
 
+H100_FULL_FORWARD_MS = 15.18     # full Pi0 forward, fused, H100 SXM5 (README.md:108)
+
+
+def main_full(args, torch):
+    """the whole Pi0Inference.forward (3 views, empty prompt, chunk 50)."""
+    from flash_vla_amd import Pi0Inference
+    from flash_vla_amd.weights import random_checkpoint
+
+    t0 = time.time()
+    ck = random_checkpoint(prompt_len=0, seed=0, device="cuda", draw_on_device=True)
+    gen = torch.Generator().manual_seed(4)
+    images = (torch.rand(3, 224, 224, 3, generator=gen) * 2 - 1).to(torch.bfloat16).cuda()
+    state = torch.randn(32, generator=gen).to(torch.bfloat16).cuda()
+    noise = torch.randn(50, 32, generator=gen).to(torch.bfloat16).cuda()
+    eng = Pi0Inference(ck, num_views=3, chunk_size=50)
+    del ck
+    print(f"[bench] full forward captured, {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    stream = torch.cuda.current_stream()
+    for _ in range(args.warmup):
+        eng.forward(images, state, noise)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(args.steps):
+        eng.forward(images, state, noise)    # copy images / state / noise, replay the graph
+    end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    print(f"[bench] full forward {ms:.3f} ms", file=sys.stderr, flush=True)
+    out = {
+        "metric": "ms per full Pi0 forward (vision + encoder + 10-step decoder, one hipGraph)",
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": round(ms / H100_FULL_FORWARD_MS, 4), "dtype": "bf16",
+        "data": "synthetic (random_checkpoint N(0,1) x 0.05 weights, uniform[-1,1] images, "
+                "N(0,1) state and noise)",
+        "config": {"workload": "Pi0 full forward, BASELINE config 4: 3 views 224x224, SigLIP "
+                               "27 layers, projector, 18-layer encoder at M=768, empty prompt, "
+                               "10-step decoder, chunk 50",
+                   "global_batch": 1, "seq_len": 768, "parallelism": "single GPU"},
+        "baseline_ms": H100_FULL_FORWARD_MS, "baseline_hw": "H100 SXM5 (published)",
+        "roofline": None, "cpu_baseline": None,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", choices=("decoder", "encoder"), default="decoder",
-                    help="decoder loop (the headline metric) or the prefix encoder")
+    ap.add_argument("--workload", choices=("decoder", "encoder", "full"), default="decoder",
+                    help="decoder loop (the headline metric), the prefix encoder, or the "
+                         "whole forward")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-kernel", action="store_true", help="skip the per-kernel roofline leg")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -238,6 +287,9 @@ def main():
 
     if args.workload == "encoder":
         main_encoder(args, torch)
+        return
+    if args.workload == "full":
+        main_full(args, torch)
         return
 
     from flash_vla_amd import Pi0DecoderEngine

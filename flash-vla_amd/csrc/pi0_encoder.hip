@@ -24,12 +24,19 @@
 //   TE_QKV_ROPE  bf16(C), RoPE on the rounded values, scatter Q / K / V
 //                                       (kernels/base.py:672-726)
 //   TE_PARTIAL   fp32 split-K partial
+//   TE_BIAS_RES  C + b + R               vision o-proj / ffn-down / patch embedding
+//                                       (kernels/base.py:197-270)
+//   TE_BIAS_GELU gelu_tanh(C + b)        vision ffn-up (kernels/base.py:273-300)
 #include "pi0_common.h"
 #include "pi0_hip.h"
 
 namespace pi0 {
 
-enum TileEpi { TE_STORE = 0, TE_BIAS = 1, TE_RES = 2, TE_GATE = 3, TE_QKV_ROPE = 4, TE_PARTIAL = 5 };
+enum TileEpi {
+  TE_STORE = 0, TE_BIAS = 1, TE_RES = 2, TE_GATE = 3, TE_QKV_ROPE = 4, TE_PARTIAL = 5,
+  TE_BIAS_RES = 6,    // C + b + R[row % res_mod or row]   (vision residual GEMMs, patch embedding)
+  TE_BIAS_GELU = 7    // gelu_tanh(C + b)                   (vision FFN up)
+};
 
 struct TileArgs {
   const __bf16* a; int lda;
@@ -39,7 +46,9 @@ struct TileArgs {
   __bf16* out_k; __bf16* out_v; int ldkv;
   const __bf16* rope;
   float* part;                          // TE_PARTIAL: [splitk][M][N] fp32
-  int M, N, K;                          // N = output columns
+  const __bf16* res; int ldres, res_mod;  // TE_BIAS_RES residual (may alias out); res_mod 0 = row
+  int n_valid;                          // output columns stored (<= N; the rest is padding)
+  int M, N, K;                          // N, K = the packed (padded) weight's shape
   int tiles_m, tiles_n, splitk, ksteps; // ksteps = 64-deep steps per split
   int heads, head_dim;
   int xcd_remap;
@@ -210,6 +219,7 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
     const f32x4 hi = *reinterpret_cast<const f32x4*>(&cs[row * CP + c + 4]);
     float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     const int col = ntile * OUTC + c;
+    if (col >= a.n_valid) continue;            // padded weight columns
     if constexpr (EPI == TE_PARTIAL) {
       float* dst = a.part + ((size_t)ks * a.M + grow) * a.N + col;
       *reinterpret_cast<f32x4*>(dst) = lo;
@@ -246,6 +256,21 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) v[q] += bf2f(rv[q]);
       }
+      if constexpr (EPI == TE_BIAS_RES || EPI == TE_BIAS_GELU) {
+        const bf16x8 b = load8(a.bias + col);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] += bf2f(b[q]);
+      }
+      if constexpr (EPI == TE_BIAS_RES) {
+        const int rrow = a.res_mod ? grow % a.res_mod : grow;
+        const bf16x8 rv = load8(a.res + (size_t)rrow * a.ldres + col);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] += bf2f(rv[q]);
+      }
+      if constexpr (EPI == TE_BIAS_GELU) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = gelu_tanh(v[q]);
+      }
     }
     bf16x8 o;
 #pragma unroll
@@ -256,23 +281,24 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
 
 // W[batch][K][N] -> 32x32x16 B fragments: tile (nt, kt) of 16 k x 32 n is 64 lanes x 8 bf16,
 // lane = (k % 16 / 8) * 32 + n % 32, element k % 8; tiles ordered [nt][kt].
+// K_pad x N_pad (multiples of 16 / 32) with zeros outside the K x N source.
 __global__ void pack_weight32_kernel(const __bf16* __restrict__ w, __bf16* __restrict__ p,
-                                     int K, int N, long long total_frags) {
+                                     int K, int N, int K_pad, int N_pad, long long total_frags) {
   const long long f = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (f >= total_frags) return;
-  const long long per = (long long)(K / 16) * (N / 32) * 64;
+  const long long per = (long long)(K_pad / 16) * (N_pad / 32) * 64;
   const long long b = f / per;
   long long rem = f - b * per;
   const int lane = (int)(rem & 63);
   rem >>= 6;
-  const int KT = K / 16;
+  const int KT = K_pad / 16;
   const int kt = (int)(rem % KT), nt = (int)(rem / KT);
   const int n = nt * 32 + (lane & 31);
   const int k0 = kt * 16 + (lane >> 5) * 8;
   const __bf16* src = w + b * (long long)K * N + (long long)k0 * N + n;
   bf16x8 v;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) v[j] = src[(long long)j * N];
+  for (int j = 0; j < 8; ++j) v[j] = (n < N && k0 + j < K) ? src[(long long)j * N] : __bf16(0.f);
   *reinterpret_cast<bf16x8*>(p + f * 8) = v;
 }
 
@@ -544,6 +570,149 @@ __global__ __launch_bounds__(256, 1) void enc_attn_kernel(EncAttnArgs a) {
     }
 }
 
+
+// ---- SigLIP vision tower pieces (pipeline.py:21-54) -----------------------------
+
+// images [views][224][224][3] -> patch rows [views * 256][ldo]: row = view * 256 + py * 16 + px,
+// column (iy * 14 + ix) * 3 + c for the 14 x 14 x 3 patch, zero for columns 588 .. ldo - 1
+// (the patchify of vision_patch_embed, wrappers.py:257-269).
+__global__ __launch_bounds__(256) void im2col_patches_kernel(const __bf16* __restrict__ img,
+                                                             __bf16* __restrict__ out, int ldo,
+                                                             int rows) {
+  const int id = blockIdx.x * 256 + threadIdx.x;
+  const int chunks = ldo >> 3;
+  const int row = id / chunks, c0 = (id - row * chunks) * 8;
+  if (row >= rows) return;
+  const int view = row >> 8, py = (row >> 4) & 15, px = row & 15;
+  bf16x8 v;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int k = c0 + j;
+    __bf16 x = __bf16(0.f);
+    if (k < 588) {
+      const int iy = k / 42, r = k - iy * 42;           // 42 = 14 columns x 3 channels
+      x = img[(((size_t)view * 224 + py * 14 + iy) * 224 + px * 14) * 3 + r];
+    }
+    v[j] = x;
+  }
+  *reinterpret_cast<bf16x8*>(out + (size_t)row * ldo + c0) = v;
+}
+
+// Multi-head vision attention (attention.py:20-26, SDPA over each view's 256 tokens,
+// 16 heads of 72). V of every (view, head) is first transposed into
+// vt[view][head][96 d][tokens] (d >= 72 zero; keys of every 16-key chunk in the P^T
+// slot order, as for the encoder), then one wave per (view, head, 32 queries) runs
+// S^T = K Q^T / O^T = V^T P^T on 32x32x16 MFMAs over the 8 key blocks (head_dim
+// zero-padded to 80 for the k16 steps), softmax in fp32 with P rounded to bf16.
+constexpr int VA_TOK = 256, VA_HD = 72, VA_HDP = 96;
+
+__global__ __launch_bounds__(256) void vision_vt_kernel(const __bf16* __restrict__ qkv, int ldqkv,
+                                                        __bf16* __restrict__ vt, int heads,
+                                                        int dim) {
+  __shared__ __bf16 tile[64][VA_HD + 1];
+  const int kc = blockIdx.x, head = blockIdx.y, view = blockIdx.z;
+  const int t = threadIdx.x;
+  const __bf16* src = qkv + ((size_t)view * VA_TOK + kc * 64) * ldqkv + 2 * dim + head * VA_HD;
+  for (int i = t; i < 64 * VA_HD; i += 256) {
+    const int kr = i / VA_HD, d = i - kr * VA_HD;
+    tile[kr][d] = src[(size_t)kr * ldqkv + d];
+  }
+  __syncthreads();
+  __bf16* dst = vt + (((size_t)view * heads + head) * VA_HDP) * VA_TOK + kc * 64;
+  for (int i = t; i < 64 * VA_HDP; i += 256) {
+    const int d = i >> 6, slot = i & 63;
+    const int sl = slot & 15, key = (slot & ~15) + ((sl & 4) ? 8 : 0) + ((sl & 8) ? 4 : 0) + (sl & 3);
+    dst[(size_t)d * VA_TOK + slot] = d < VA_HD ? tile[key][d] : __bf16(0.f);
+  }
+}
+
+struct VisAttnArgs {
+  const __bf16* qkv; int ldqkv;
+  const __bf16* vt;
+  __bf16* out; int ldo;
+  int heads, dim;
+  float scale_log2;
+};
+
+__global__ __launch_bounds__(64) void vision_attn_kernel(VisAttnArgs a) {
+  const int lane = threadIdx.x, r = lane & 31, h = lane >> 5;
+  const int qt = blockIdx.x, head = blockIdx.y, view = blockIdx.z;
+  const size_t row0 = (size_t)view * VA_TOK;
+  const int q = qt * 32 + r;
+  // Q^T fragments: lane holds Q[q][16 kk + 8 h .. + 7] (zero past d = 72)
+  bf16x8 qf[5];
+#pragma unroll
+  for (int kk = 0; kk < 5; ++kk) {
+    const int d = kk * 16 + h * 8;
+    qf[kk] = d < VA_HD ? load8(a.qkv + (row0 + q) * a.ldqkv + head * VA_HD + d) : zero8();
+  }
+  float m_run = -1.0e30f, l_run = 0.f;
+  f32x16 o[3];
+#pragma unroll
+  for (int dt = 0; dt < 3; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+  const __bf16* vt = a.vt + (((size_t)view * a.heads + head) * VA_HDP) * VA_TOK;
+  for (int kb = 0; kb < VA_TOK / 32; ++kb) {
+    bf16x8 kf[5];
+#pragma unroll
+    for (int kk = 0; kk < 5; ++kk) {
+      const int d = kk * 16 + h * 8;
+      kf[kk] = d < VA_HD ? load8(a.qkv + (row0 + kb * 32 + r) * a.ldqkv + a.dim + head * VA_HD + d)
+                         : zero8();
+    }
+    bf16x8 vf[3][2];
+#pragma unroll
+    for (int dt = 0; dt < 3; ++dt)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+        vf[dt][c] = load8(vt + (size_t)(dt * 32 + r) * VA_TOK + kb * 32 + 16 * c + 8 * h);
+    f32x16 st;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) st[e] = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 5; ++kk) st = mfma32(kf[kk], qf[kk], st);
+    float mx = -1.0e30f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) { st[e] *= a.scale_log2; mx = fmaxf(mx, st[e]); }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, PI0_WAVE));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = fast_exp2(m_run - m_new);
+    float ps = 0.f;
+    bf16x8 pf[2];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float pv = fast_exp2(st[e] - m_new);
+      ps += pv;
+      pf[e >> 3][e & 7] = f2bf(pv);
+    }
+    ps += __shfl_xor(ps, 32, PI0_WAVE);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+#pragma unroll
+    for (int dt = 0; dt < 3; ++dt) {
+      f32x16 acc = o[dt] * alpha;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) acc = mfma32(vf[dt][c], pf[c], acc);
+      o[dt] = acc;
+    }
+  }
+  // lane holds O^T[d = 32 dt + 8 (e / 4) + 4 h + e % 4][query r]
+  const float inv = __builtin_amdgcn_rcpf(l_run);
+  __bf16* orow = a.out + (row0 + q) * a.ldo + head * VA_HD;
+#pragma unroll
+  for (int dt = 0; dt < 3; ++dt)
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) {
+      const int d = dt * 32 + 8 * e4 + 4 * h;
+      if (d < VA_HD) {
+        const bf16x4 pk = {f2bf(o[dt][e4 * 4] * inv), f2bf(o[dt][e4 * 4 + 1] * inv),
+                           f2bf(o[dt][e4 * 4 + 2] * inv), f2bf(o[dt][e4 * 4 + 3] * inv)};
+        *reinterpret_cast<bf16x4*>(orow + d) = pk;
+      }
+    }
+}
+
 }  // namespace pi0
 
 using namespace pi0;
@@ -583,7 +752,7 @@ static TileArgs tile_args(const void* x, int ldx, const void* w, void* out, int 
   TileArgs a = {};
   a.a = (const __bf16*)x; a.lda = ldx; a.w0 = (const __bf16*)w;
   a.out = (__bf16*)out; a.ldo = ldo;
-  a.M = M; a.N = N; a.K = K; a.splitk = 1;
+  a.M = M; a.N = N; a.K = K; a.splitk = 1; a.n_valid = N;
   return a;
 }
 
@@ -597,12 +766,18 @@ static bool misaligned(const void* p, int ld) {
 extern "C" {
 
 int pi0hip_pack_weight32(const void* w, void* packed, int K, int N, int batch, hipStream_t s) {
+  if (K % 16 || N % 32) return (K <= 0 || N <= 0) ? PI0HIP_ERR_ARG : PI0HIP_ERR_SHAPE;
+  return pi0hip_pack_weight32_padded(w, packed, K, N, K, N, batch, s);
+}
+
+int pi0hip_pack_weight32_padded(const void* w, void* packed, int K, int N, int K_pad, int N_pad,
+                                int batch, hipStream_t s) {
   if (!w || !packed || K <= 0 || N <= 0 || batch <= 0) return PI0HIP_ERR_ARG;
-  if (K % 16 || N % 32) return PI0HIP_ERR_SHAPE;
-  const long long frags = (long long)batch * (K / 16) * (N / 32) * 64;
+  if (K_pad % 16 || N_pad % 32 || K_pad < K || N_pad < N) return PI0HIP_ERR_SHAPE;
+  const long long frags = (long long)batch * (K_pad / 16) * (N_pad / 32) * 64;
   const long long blocks = (frags + 255) / 256;
   hipLaunchKernelGGL(pack_weight32_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
-                     (const __bf16*)w, (__bf16*)packed, K, N, frags);
+                     (const __bf16*)w, (__bf16*)packed, K, N, K_pad, N_pad, frags);
   return (int)hipGetLastError();
 }
 
@@ -708,6 +883,72 @@ int pi0hip_encoder_attention(const void* q, int ldq, const void* k, const void* 
   a.rows = rows; a.keys = keys;
   a.scale_log2 = 1.4426950408889634f * scale;
   hipLaunchKernelGGL(enc_attn_kernel, dim3((rows + 31) / 32), dim3(256), 0, s, a);
+  return (int)hipGetLastError();
+}
+
+int pi0hip_tile_linear_bias_res(const void* x, int ldx, const void* w_packed, const void* bias,
+                                const void* res, int ldres, int res_mod, void* out, int ldo, int M,
+                                int N, int K, int N_pad, int K_pad, hipStream_t s) {
+  if (!x || !w_packed || !bias || !res || !out || bad_dims(M, N, K) || res_mod < 0)
+    return PI0HIP_ERR_ARG;
+  if (N_pad < N || K_pad < K || N % 8 || misaligned(x, ldx) || misaligned(out, ldo) ||
+      misaligned(res, ldres) || misaligned(bias, 0))
+    return PI0HIP_ERR_SHAPE;
+  TileArgs a = tile_args(x, ldx, w_packed, out, ldo, M, N_pad, K_pad);
+  a.n_valid = N;
+  a.bias = (const __bf16*)bias;
+  a.res = (const __bf16*)res; a.ldres = ldres; a.res_mod = res_mod;
+  return launch_tile_auto<32, 32, 8, TE_BIAS_RES, false>(a, s);
+}
+
+int pi0hip_tile_linear_bias_gelu(const void* x, int ldx, const void* w_packed, const void* bias,
+                                 void* out, int ldo, int M, int N, int K, int N_pad, int K_pad,
+                                 hipStream_t s) {
+  if (!x || !w_packed || !bias || !out || bad_dims(M, N, K)) return PI0HIP_ERR_ARG;
+  if (N_pad < N || K_pad < K || N % 8 || misaligned(x, ldx) || misaligned(out, ldo) ||
+      misaligned(bias, 0))
+    return PI0HIP_ERR_SHAPE;
+  TileArgs a = tile_args(x, ldx, w_packed, out, ldo, M, N_pad, K_pad);
+  a.n_valid = N;
+  a.bias = (const __bf16*)bias;
+  return launch_tile_auto<64, 32, 8, TE_BIAS_GELU, false>(a, s);
+}
+
+int pi0hip_im2col_patches(const void* images, int views, void* out, int ldo, hipStream_t s) {
+  if (!images || !out || views <= 0) return PI0HIP_ERR_ARG;
+  if (ldo < 588 || ldo % 8 || misaligned(out, ldo)) return PI0HIP_ERR_SHAPE;
+  const int rows = views * 256;
+  const int threads = rows * (ldo / 8);
+  hipLaunchKernelGGL(im2col_patches_kernel, dim3((threads + 255) / 256), dim3(256), 0, s,
+                     (const __bf16*)images, (__bf16*)out, ldo, rows);
+  return (int)hipGetLastError();
+}
+
+size_t pi0hip_vision_attention_workspace_bytes(int views, int heads) {
+  if (views <= 0 || heads <= 0) return 0;
+  return round256_((size_t)views * heads * VA_HDP * VA_TOK * sizeof(__bf16));
+}
+
+int pi0hip_vision_attention(const void* qkv, int ldqkv, void* out, int ldo, int views, int tokens,
+                            int heads, int head_dim, float scale, void* ws, size_t ws_bytes,
+                            hipStream_t s) {
+  if (!qkv || !out || views <= 0 || heads <= 0) return PI0HIP_ERR_ARG;
+  const int dim = heads * head_dim;
+  if (tokens != VA_TOK || head_dim != VA_HD || ldqkv < 3 * dim || ldo < dim ||
+      misaligned(qkv, ldqkv) || (ldo & 3) || (reinterpret_cast<uintptr_t>(out) & 7))
+    return PI0HIP_ERR_SHAPE;
+  if (!ws || ws_bytes < pi0hip_vision_attention_workspace_bytes(views, heads))
+    return PI0HIP_ERR_WORKSPACE;
+  hipLaunchKernelGGL(vision_vt_kernel, dim3(VA_TOK / 64, heads, views), dim3(256), 0, s,
+                     (const __bf16*)qkv, ldqkv, (__bf16*)ws, heads, dim);
+  if (hipError_t e = hipGetLastError()) return (int)e;
+  VisAttnArgs a = {};
+  a.qkv = (const __bf16*)qkv; a.ldqkv = ldqkv;
+  a.vt = (const __bf16*)ws;
+  a.out = (__bf16*)out; a.ldo = ldo;
+  a.heads = heads; a.dim = dim;
+  a.scale_log2 = 1.4426950408889634f * scale;
+  hipLaunchKernelGGL(vision_attn_kernel, dim3(VA_TOK / 32, heads, views), dim3(64), 0, s, a);
   return (int)hipGetLastError();
 }
 

@@ -7,7 +7,7 @@ The public names follow the reference package facade (`src/flash_vla/__init__.py
 """
 from __future__ import annotations
 
-__all__ = ["Pi0DecoderEngine", "Pi0EncoderEngine", "random_checkpoint", "decoder_checkpoint", "decoder_inputs",
+__all__ = ["Pi0Inference", "Pi0DecoderEngine", "Pi0EncoderEngine", "random_checkpoint", "decoder_checkpoint", "decoder_inputs",
            "op_table"]
 
 
@@ -22,6 +22,8 @@ def __getattr__(name: str):
         from .engine import Pi0DecoderEngine as value
     elif name == "Pi0EncoderEngine":
         from .engine import Pi0EncoderEngine as value
+    elif name == "Pi0Inference":
+        from .engine import Pi0Inference as value
     else:
         raise AttributeError(f"module {__name__!r} has no attribute {name!r}")
     globals()[name] = value

@@ -37,6 +37,7 @@ PROTOTYPES = {
                                  c_int, P, c_size_t, P]),
     # prefix encoder
     "pi0hip_pack_weight32": (c_int, [P, P, c_int, c_int, c_int, P]),
+    "pi0hip_pack_weight32_padded": (c_int, [P, P, c_int, c_int, c_int, c_int, c_int, P]),
     "pi0hip_rms_norm": (c_int, [P, c_int, P, c_int, c_int, c_int, P]),
     "pi0hip_layer_norm": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_float, P]),
     "pi0hip_tile_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
@@ -49,6 +50,15 @@ PROTOTYPES = {
     "pi0hip_encoder_attention_workspace_bytes": (c_size_t, [c_int]),
     "pi0hip_encoder_attention": (c_int, [P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int,
                                          c_float, P, c_size_t, P]),
+    # vision tower
+    "pi0hip_tile_linear_bias_res": (c_int, [P, c_int, P, P, P, c_int, c_int, P, c_int, c_int,
+                                            c_int, c_int, c_int, c_int, P]),
+    "pi0hip_tile_linear_bias_gelu": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int,
+                                             c_int, c_int, P]),
+    "pi0hip_im2col_patches": (c_int, [P, c_int, P, c_int, P]),
+    "pi0hip_vision_attention_workspace_bytes": (c_size_t, [c_int, c_int]),
+    "pi0hip_vision_attention": (c_int, [P, c_int, P, c_int, c_int, c_int, c_int, c_int, c_float,
+                                        P, c_size_t, P]),
 }
 
 ERRORS = {-1: "invalid argument", -2: "unsupported shape", -3: "workspace missing or too small"}

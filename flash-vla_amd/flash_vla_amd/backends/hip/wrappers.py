@@ -72,10 +72,10 @@ def _ptr(t: torch.Tensor):
 # and looked up by address on every later call.
 # ---------------------------------------------------------------------------
 class _PackedEntry:
-    __slots__ = ("src", "packed", "base", "nbytes", "K", "N", "version", "layout")
+    __slots__ = ("src", "packed", "base", "nbytes", "K", "N", "version", "layout", "pad")
 
-    def __init__(self, src, packed, K, N, layout):
-        self.src, self.packed, self.K, self.N, self.layout = src, packed, K, N, layout
+    def __init__(self, src, packed, K, N, layout, pad):
+        self.src, self.packed, self.K, self.N, self.layout, self.pad = src, packed, K, N, layout, pad
         self.base = src.data_ptr()
         self.nbytes = src.numel() * src.element_size()
         self.version = src._version
@@ -87,51 +87,73 @@ _PACKED: list[_PackedEntry] = []
 _PACKERS = {16: "pi0hip_pack_weight", 32: "pi0hip_pack_weight32"}
 
 
-def _pack_into(src: torch.Tensor, dst: torch.Tensor, K: int, N: int, layout: int) -> None:
+def _pack_into(src: torch.Tensor, dst: torch.Tensor, K: int, N: int, layout: int, pad) -> None:
     batch = src.numel() // (K * N)
-    _abi.call(_PACKERS[layout], _ptr(src), _ptr(dst), K, N, batch, _stream())
+    if pad is not None:
+        _abi.call("pi0hip_pack_weight32_padded", _ptr(src), _ptr(dst), K, N, pad[0], pad[1], batch,
+                  _stream())
+    else:
+        _abi.call(_PACKERS[layout], _ptr(src), _ptr(dst), K, N, batch, _stream())
 
 
-def packed_weight_ptr(w: torch.Tensor, layout: int = 16) -> int:
+def packed_weight_ptr(w: torch.Tensor, layout: int = 16, pad: tuple | None = None) -> int:
     """Device address of the packed copy of `w` ([K, N] bf16, possibly a layer view).
 
     layout 16: the decoder kernels' 32 k x 16 n fragments (pi0hip_pack_weight);
-    layout 32: the encoder kernels' 16 k x 32 n fragments (pi0hip_pack_weight32)."""
+    layout 32: the encoder kernels' 16 k x 32 n fragments (pi0hip_pack_weight32);
+    pad = (K_pad, N_pad): layout 32 zero-padded to whole tiles (pi0hip_pack_weight32_padded)."""
     _check(w, "weight", 2)
     if not w.is_contiguous():
         raise ValueError("weight must be contiguous [K, N]")
     K, N = w.shape
+    if pad is not None:
+        pad = (int(pad[0]), int(pad[1]))
+        if layout != 32 or pad == (K, N):
+            pad = None if pad == (K, N) else pad
+        if pad is not None and (pad[0] < K or pad[1] < N):
+            raise ValueError("padding smaller than the weight")
+    scale = 1 if pad is None else (pad[0] * pad[1]) / (K * N)
     ptr = w.data_ptr()
     for e in _PACKED:
-        if e.K == K and e.N == N and e.layout == layout and e.base <= ptr < e.base + e.nbytes:
+        if (e.K == K and e.N == N and e.layout == layout and e.pad == pad
+                and e.base <= ptr < e.base + e.nbytes):
             if not _capturing() and e.version != e.src._version:
-                _pack_into(e.src, e.packed, K, N, layout)
+                _pack_into(e.src, e.packed, K, N, layout, pad)
                 e.version = e.src._version
-            return e.packed.data_ptr() + (ptr - e.base)
+            return e.packed.data_ptr() + int((ptr - e.base) * scale)
     if _capturing():
         raise RuntimeError("weight was not packed before graph capture; run a warmup pass first")
     base = w._base if w._base is not None else w
     src = base if (base.dim() >= 2 and base.is_contiguous() and tuple(base.shape[-2:]) == (K, N)
                    and base.dtype == w.dtype) else w
-    packed = torch.empty_like(src)
-    _pack_into(src, packed, K, N, layout)
-    entry = _PackedEntry(src, packed, K, N, layout)
+    if pad is None:
+        packed = torch.empty_like(src)
+    else:
+        packed = torch.empty(src.numel() // (K * N) * pad[0] * pad[1], dtype=src.dtype,
+                             device=src.device)
+    _pack_into(src, packed, K, N, layout, pad)
+    entry = _PackedEntry(src, packed, K, N, layout, pad)
     _PACKED.append(entry)
-    return packed.data_ptr() + (ptr - entry.base)
+    return packed.data_ptr() + int((ptr - entry.base) * scale)
 
 
 def prepare_weights(weights: dict) -> None:
-    """Pack every 2-D/3-D GEMM weight of the decoder and encoder up front (outside any capture)."""
-    names = {16: ("decoder_action_mlp_w", "decoder_attn_qkv_w", "decoder_attn_o_w",
-                  "decoder_ffn_gate_w", "decoder_ffn_up_w", "decoder_ffn_down_w",
-                  "decoder_action_fused_out_proj_w"),
-             32: ("encoder_multi_modal_projector_w", "encoder_attn_qkv_w", "encoder_attn_o_w",
-                  "encoder_ffn_gate_w", "encoder_ffn_up_w", "encoder_ffn_down_w")}
-    for layout, group in names.items():
-        for name in group:
-            if name in weights:
-                w = weights[name]
-                packed_weight_ptr(w if w.dim() == 2 else w[0], layout)
+    """Pack every GEMM weight stack of the model up front (outside any capture)."""
+    plan = {name: (16, None) for name in (
+        "decoder_action_mlp_w", "decoder_attn_qkv_w", "decoder_attn_o_w", "decoder_ffn_gate_w",
+        "decoder_ffn_up_w", "decoder_ffn_down_w", "decoder_action_fused_out_proj_w")}
+    plan.update({name: (32, None) for name in (
+        "encoder_multi_modal_projector_w", "encoder_attn_qkv_w", "encoder_attn_o_w",
+        "encoder_ffn_gate_w", "encoder_ffn_up_w", "encoder_ffn_down_w",
+        "vision_attn_qkv_w", "vision_attn_o_w")})
+    plan["vision_ffn_up_w"] = (32, (1152, 4352))
+    plan["vision_ffn_down_w"] = (32, (4352, 1152))
+    for name, (layout, pad) in plan.items():
+        if name in weights:
+            w = weights[name]
+            packed_weight_ptr(w if w.dim() == 2 else w[0], layout, pad)
+    if "vision_patch_embedding_w" in weights:
+        packed_weight_ptr(weights["vision_patch_embedding_w"].reshape(588, 1152), 32, (640, 1152))
 
 
 def clear_packed_cache() -> None:

@@ -89,3 +89,29 @@ def allocate_encoder_buffers(encoder_seq_len: int, device, buffers: dict | None 
         buffers["encoder_V"] = buf(layers, cache_len, head_dim)
     buffers["encoder_rope_weights"].copy_(rope_table(encoder_seq_len, 0, head_dim, device))
     return buffers
+
+
+def allocate_static_buffers(num_views: int, chunk_size: int, prompt_len: int, device,
+                            vision_layers: int | None = None) -> tuple[dict, int]:
+    """Every persistent buffer of the full forward (buffers.py:25-64 of the reference):
+    images, state, noise, vision, encoder and decoder buffers, the K/V cache sized for
+    prefix + decoder rows, and both RoPE tables. Returns (buffers, encoder_seq_len)."""
+    del vision_layers
+    bf16 = torch.bfloat16
+    encoder_seq_len = num_views * 256 + prompt_len
+    buffers = allocate_decoder_buffers(encoder_seq_len, chunk_size, device)
+    cache_len = encoder_seq_len + chunk_size + 1
+    allocate_encoder_buffers(encoder_seq_len, device, buffers=buffers, cache_len=cache_len,
+                             num_views=num_views)
+
+    def buf(*shape):
+        return torch.zeros(shape, dtype=bf16, device=device)
+
+    buffers.update({
+        "observation_images_normalized": buf(num_views, 224, 224, 3),
+        "vision_x": buf(num_views, 256, VISION_WIDTH),
+        "vision_x_norm": buf(num_views, 256, VISION_WIDTH),
+        "vision_QKV": buf(num_views, 256, 3 * VISION_WIDTH),
+        "vision_hidden": buf(num_views, 256, 4304),
+    })
+    return buffers, encoder_seq_len

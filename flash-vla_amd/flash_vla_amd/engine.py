@@ -18,9 +18,9 @@ import torch
 from . import pipeline
 from .arena import ScratchPool
 from .backends import BACKENDS
-from .buffers import allocate_decoder_buffers, allocate_encoder_buffers
+from .buffers import allocate_decoder_buffers, allocate_encoder_buffers, allocate_static_buffers
 from .ops import op_table
-from .spec import DECODER_WEIGHT_NAMES, decoder_weight_shapes
+from .spec import DECODER_WEIGHT_NAMES, decoder_weight_shapes, weight_shapes
 
 
 class Pi0DecoderEngine:
@@ -186,6 +186,102 @@ class Pi0EncoderEngine:
 
     def replay(self) -> None:
         self.graph.replay()
+
+
+class Pi0Inference:
+    """One captured Pi0 forward pass: vision tower, prefix encoder and the 10-step
+    decoder loop in one hipGraph (`hardware/nvidia/h100/pi0/engine.py:26-86`).
+
+    `steps` and `layers` (decoder), `vision_layers` and `encoder_layers` exist for
+    bisection, as in the reference. With `fp32_euler` (default) the Euler
+    accumulator is an fp32 copy of `diffusion_noise`, seeded inside the graph and
+    rounded into the bf16 output once at the end.
+    """
+
+    def __init__(self, checkpoint: dict, num_views: int = 3, chunk_size: int = 50,
+                 steps: int = 10, layers: int = 18, fused: bool = True, device: str = "cuda",
+                 backend: str = "hip", plan: dict | None = None, fp32_euler: bool = True,
+                 vision_layers: int | None = None, encoder_layers: int | None = None,
+                 capture: bool = True, warmup: int = 3):
+        self.num_views = num_views
+        self.chunk_size = chunk_size
+        self.steps = steps
+        self.layers = layers
+        self.vision_layers = vision_layers
+        self.encoder_layers = encoder_layers
+        self.ops = op_table(fused, backend=backend, plan=plan)
+        self.backend = BACKENDS[backend]
+        self.prompt_len = len(checkpoint["language_embeds"])
+        bf16 = torch.bfloat16
+        shapes = weight_shapes(self.prompt_len)
+        self.weights = {}
+        for name, shape in shapes.items():
+            src = checkpoint[name]
+            got = tuple(src.shape)
+            # per-layer stacks may hold fewer layers than the model (shallow test models)
+            stacked = name.startswith(("vision_attn", "vision_ffn", "vision_pre", "encoder_attn",
+                                       "encoder_ffn", "decoder_attn", "decoder_ffn"))
+            ok = got == tuple(shape) or (stacked and got[1:] == tuple(shape[1:]) and got[0] >= 1)
+            if not ok:
+                raise ValueError(f"{name}: shape {got}, expected {tuple(shape)}")
+            self.weights[name] = torch.empty(got, dtype=bf16, device=device)
+            self.weights[name].copy_(src)
+        self.layers = min(self.layers, self.weights["decoder_attn_qkv_w"].shape[0])
+        self.buffers, self.encoder_seq_len = allocate_static_buffers(
+            num_views, chunk_size, self.prompt_len, device)
+        if fp32_euler:
+            self.buffers["diffusion_noise_f32"] = torch.zeros(
+                chunk_size, shapes["decoder_state_in_proj_w"][0], dtype=torch.float32,
+                device=device)
+        self.pool = ScratchPool()
+        self.graph = None
+        if hasattr(self.backend, "prepare_weights"):
+            self.backend.prepare_weights(self.weights)
+        if capture:
+            self._capture(warmup)
+
+    def _run(self):
+        """One full forward pass, in place on the static buffers (engine.py:58-65)."""
+        b = self.buffers
+        if self.prompt_len:
+            b["encoder_x"][self.num_views * 256:].copy_(self.weights["language_embeds"])
+        if "diffusion_noise_f32" in b:
+            b["diffusion_noise_f32"].copy_(b["diffusion_noise"])
+        with self.backend.use_pool(self.pool):
+            pipeline.vision_encoder(self.ops, self.weights, b, self.num_views,
+                                    layers=self.vision_layers)
+            pipeline.transformer_encoder(self.ops, self.weights, b, self.encoder_seq_len,
+                                         layers=self.encoder_layers)
+            pipeline.transformer_decoder(self.ops, self.weights, b, self.encoder_seq_len,
+                                         steps=self.steps, layers=self.layers)
+
+    def _capture(self, warmup: int):
+        saved = self.buffers["diffusion_noise"].clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                self.buffers["diffusion_noise"].copy_(saved)
+                self._run()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self.pool.freeze()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._run()
+        torch.cuda.synchronize()
+        self.buffers["diffusion_noise"].copy_(saved)
+
+    def forward(self, images, state, noise):
+        """Copy inputs into the static buffers, replay, return the denoised chunk (engine.py:80-86)."""
+        self.buffers["observation_images_normalized"].copy_(images)
+        self.buffers["observation_state_normalized"].copy_(state)
+        self.buffers["diffusion_noise"].copy_(noise)
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self._run()
+        return self.buffers["diffusion_noise"]
 
 
 def _dims_from(weights: dict) -> dict:

@@ -15,7 +15,40 @@ from __future__ import annotations
 from .spec import HEAD_DIM
 
 
-def transformer_encoder(ops, weights, buffers, encoder_seq_len, layers=18, project=True):
+def vision_encoder(ops, weights, buffers, num_views, layers=None):
+    """Patch-embed the images and run the SigLIP layers, in place on `vision_x`
+    (pipeline.py:21-54). `ops.vision_attention` is the op-table form of the
+    function the reference pipeline calls directly (`kernels/attention.py:20-26`)."""
+    if num_views == 2:
+        raise ValueError("the num_views == 2 two-part vision branch is not implemented "
+                         "(as in the reference, pipeline.py:23)")
+    ops.vision_patch_embed(
+        buffers["observation_images_normalized"], weights["vision_patch_embedding_w"],
+        weights["vision_patch_embedding_b"], weights["vision_position_embedding"],
+        buffers["vision_x"])
+    n = weights["vision_attn_qkv_w"].shape[0] if layers is None else layers
+    for i in range(n):
+        ops.vision_norm_qkv(
+            buffers["vision_x"],
+            weights["vision_pre_attn_norm_w"][i], weights["vision_pre_attn_norm_b"][i],
+            weights["vision_attn_qkv_w"][i], weights["vision_attn_qkv_b"][i],
+            buffers["vision_QKV"], buffers["vision_x_norm"])
+        attn = ops.vision_attention(buffers["vision_QKV"])
+        ops.vision_out_proj_residual(
+            attn, weights["vision_attn_o_w"][i], weights["vision_attn_o_b"][i],
+            buffers["vision_x"], buffers["vision_x"])
+        ops.vision_norm_ffn_up(
+            buffers["vision_x"],
+            weights["vision_pre_ffn_norm_w"][i], weights["vision_pre_ffn_norm_b"][i],
+            weights["vision_ffn_up_w"][i], weights["vision_ffn_up_b"][i],
+            buffers["vision_hidden"], buffers["vision_x_norm"])
+        ops.vision_ffn_down_residual(
+            buffers["vision_hidden"],
+            weights["vision_ffn_down_w"][i], weights["vision_ffn_down_b"][i],
+            buffers["vision_x"], buffers["vision_x"])
+
+
+def transformer_encoder(ops, weights, buffers, encoder_seq_len, layers=None, project=True):
     """Prefix encoder (pipeline.py:57-89): optional vision projector, then the Gemma layers.
 
     The last layer runs only its norm + QKV + RoPE: only its K and V are read
@@ -32,6 +65,8 @@ def transformer_encoder(ops, weights, buffers, encoder_seq_len, layers=18, proje
             buffers["encoder_x"], buffers["vision_x_norm"])
 
     scale = HEAD_DIM ** -0.5
+    if layers is None:
+        layers = weights["encoder_attn_qkv_w"].shape[0]
     for i in range(layers):
         ops.encoder_norm_qkv_rope(
             buffers["encoder_x"], weights["encoder_attn_qkv_w"][i],

@@ -33,15 +33,19 @@ def _gen(seed: int) -> torch.Generator:
 
 
 def random_checkpoint(num_views: int = 3, chunk_size: int = 50, prompt_len: int = 256,
-                      wscale: float = 0.05, seed: int = 0, device: str = "cuda") -> dict:
-    """Synthetic packed checkpoint, N(0,1)*wscale per tensor in schema order."""
+                      wscale: float = 0.05, seed: int = 0, device: str = "cuda",
+                      draw_on_device: bool = False) -> dict:
+    """Synthetic packed checkpoint, N(0,1)*wscale per tensor in schema order.
+
+    `draw_on_device=True` draws on `device`'s own seeded generator (fast for the
+    2.7 B-parameter model; the values then differ from the CPU draw)."""
     del num_views, chunk_size
-    gen = _gen(seed)
-    return {
-        name: (torch.randn(shape, dtype=torch.float32, generator=gen) * wscale)
-        .to(torch.bfloat16).to(device)
-        for name, shape in weight_shapes(prompt_len).items()
-    }
+    gen = (torch.Generator(device=device).manual_seed(seed) if draw_on_device else _gen(seed))
+    out = {}
+    for name, shape in weight_shapes(prompt_len).items():
+        t = torch.randn(shape, dtype=torch.float32, generator=gen, device=gen.device) * wscale
+        out[name] = t.to(torch.bfloat16).to(device)
+    return out
 
 
 def openpi_decoder_params(seed: int = 0, std: float = 0.02, layers: int = DECODER_LAYERS,

@@ -117,6 +117,12 @@ int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int l
  * relayout, like pi0hip_pack_weight (no reference counterpart). */
 int pi0hip_pack_weight32(const void* w, void* packed, int K, int N, int batch, hipStream_t s);
 
+/* pi0hip_pack_weight32 into a K_pad x N_pad packed block (K_pad % 16 == 0,
+ * N_pad % 32 == 0), zero outside the K x N source: lets GEMMs with ragged K / N
+ * (the vision FFN's 4304, the 588-wide patches) run on whole tiles. */
+int pi0hip_pack_weight32_padded(const void* w, void* packed, int K, int N, int K_pad, int N_pad,
+                                int batch, hipStream_t s);
+
 /* out = bf16(x * rsqrt(mean(x^2) + 1e-6)), one row per wave; K in {1024, 2048}.
  * tl_rms_norm, kernels/base.py:373-403 (encoder_norm_qkv_rope / encoder_norm_gated_ffn,
  * wrappers.py:347-381) */
@@ -169,6 +175,39 @@ size_t pi0hip_encoder_attention_workspace_bytes(int keys);
 int pi0hip_encoder_attention(const void* q, int ldq, const void* k, const void* v, int ldkv,
                              void* out, int ldo, int rows, int keys, int head_dim, float scale,
                              void* ws, size_t ws_bytes, hipStream_t s);
+
+/* ---- SigLIP vision tower (M = views x 256 rows, width 1152, 16 heads of 72) ---- */
+
+/* out = x @ W + bias + res[r], r = row % res_mod (res_mod > 0) or row; `res` may
+ * alias `out`. W packed by pi0hip_pack_weight32_padded to K_pad x N_pad (N_pad %
+ * 128 == 0, K_pad % 128 == 0); only the N valid columns are stored (N % 8 == 0).
+ * vision_out_proj_residual / vision_ffn_down_residual / vision_patch_embed
+ * (wrappers.py:252-313; tl_matmul_bias_res / _mod, kernels/base.py:197-270) */
+int pi0hip_tile_linear_bias_res(const void* x, int ldx, const void* w_packed, const void* bias,
+                                const void* res, int ldres, int res_mod, void* out, int ldo, int M,
+                                int N, int K, int N_pad, int K_pad, hipStream_t s);
+
+/* out = gelu_tanh(x @ W + bias), same padding rules.
+ * vision_norm_ffn_up GEMM (wrappers.py:292-299; tl_matmul_bias_gelu, kernels/base.py:273-300) */
+int pi0hip_tile_linear_bias_gelu(const void* x, int ldx, const void* w_packed, const void* bias,
+                                 void* out, int ldo, int M, int N, int K, int N_pad, int K_pad,
+                                 hipStream_t s);
+
+/* images [views][224][224][3] -> patch rows [views*256][ldo] (14 x 14 x 3 features in
+ * (iy, ix, c) order, zero-filled from column 588 to ldo); ldo % 8 == 0, ldo >= 588.
+ * The patchify of vision_patch_embed (wrappers.py:257-269). */
+int pi0hip_im2col_patches(const void* images, int views, void* out, int ldo, hipStream_t s);
+
+/* Workspace of pi0hip_vision_attention: per-head transposed V. */
+size_t pi0hip_vision_attention_workspace_bytes(int views, int heads);
+
+/* Per view and head: out = softmax(scale * q k^T) v over the view's 256 tokens, q / k / v
+ * read from the packed QKV rows [views*256][ldqkv] (q | k | v, heads x 72 each); out
+ * [views*256][ldo] in head-major columns. tokens must be 256, head_dim 72.
+ * vision_attention, kernels/attention.py:20-26 */
+int pi0hip_vision_attention(const void* qkv, int ldqkv, void* out, int ldo, int views, int tokens,
+                            int heads, int head_dim, float scale, void* ws, size_t ws_bytes,
+                            hipStream_t s);
 
 #ifdef __cplusplus
 }

@@ -85,3 +85,34 @@ def test_layer_norm_matches_torch():
     b = torch.randn(48, generator=g, dtype=torch.float64)
     ref = torch.nn.functional.layer_norm(x, (48,), w, b, eps=1e-5)
     assert torch.allclose(E.enc_layer_norm(x, w, b, bf16=False), ref, atol=1e-10)
+
+
+# ---- vision tower pins ---------------------------------------------------------------
+from oracle import pi0_vision as Vn
+
+
+def test_patch_embed_is_a_14x14_stride_14_convolution():
+    """The GEMM over (iy, ix, c) patches == conv2d with the [14, 14, 3, D] kernel."""
+    g = torch.Generator().manual_seed(11)
+    img = torch.randn(2, 224, 224, 3, generator=g, dtype=torch.float64)
+    w = torch.randn(14, 14, 3, 1152, generator=g, dtype=torch.float64) * 0.05
+    b = torch.randn(1152, generator=g, dtype=torch.float64)
+    pos = torch.randn(256, 1152, generator=g, dtype=torch.float64)
+    got = Vn.patch_embed(img, w, b, pos, bf16=False).reshape(2, 16, 16, 1152)
+    conv = torch.nn.functional.conv2d(img.permute(0, 3, 1, 2), w.permute(3, 2, 0, 1), b, stride=14)
+    ref = conv.permute(0, 2, 3, 1) + pos.reshape(16, 16, 1152)
+    assert torch.allclose(got, ref, atol=1e-9)
+
+
+def test_vision_attention_brute_force():
+    g = torch.Generator().manual_seed(12)
+    qkv = torch.randn(2 * 256, 3 * 1152, generator=g, dtype=torch.float64)
+    got = Vn.vision_attention(qkv, 2, bf16=False)
+    for view, head, t in ((0, 0, 0), (1, 15, 255), (1, 7, 100)):
+        rows = qkv[view * 256:(view + 1) * 256]
+        q = rows[t, head * 72:(head + 1) * 72]
+        k = rows[:, 1152 + head * 72:1152 + (head + 1) * 72]
+        v = rows[:, 2304 + head * 72:2304 + (head + 1) * 72]
+        s = k @ q / math.sqrt(72)
+        p = torch.exp(s - s.max()); p = p / p.sum()
+        assert torch.allclose(got[view * 256 + t, head * 72:(head + 1) * 72], p @ v)
