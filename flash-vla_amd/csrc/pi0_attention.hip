@@ -38,9 +38,21 @@ struct AttnArgs {
   const __bf16* k; const __bf16* v; int ldkv;
   __bf16* out; int ldo;
   float* part; float* lse;
-  int rows, keys, enc_len, heads, nchunks, rows_pad, nqt;
+  int rows, keys, enc_len, heads, nchunks, rows_pad, nqt;   // rows / keys per request
   float scale_log2;
+  int batch;                 // requests (grid.y); request b reads K / V at b * kv_bstride
+  long long kv_bstride;
 };
+
+// Output row of local flat row lr (= token * heads + head) of request b: the tokens of a
+// batch are stored "states first" (B state tokens, then B x T action tokens), the order
+// the decoder's residual stream uses; for one request this is the identity.
+__device__ __forceinline__ int out_row(const AttnArgs& a, int b, int lr) {
+  const int t = lr / a.heads, head = lr - t * a.heads;
+  const int T = a.rows / a.heads - 1;
+  const int tok = t == 0 ? b : a.batch + b * T + (t - 1);
+  return tok * a.heads + head;
+}
 
 __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) __bf16 ks_[ATT_CH][KP];   // reused as O buffer
@@ -52,6 +64,12 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
   const int r = lane & 15, g = lane >> 4;
   const int qt = blockIdx.x % a.nqt, c = blockIdx.x / a.nqt;
   const int q0 = qt * ATT_QT, k0 = c * ATT_CH;
+  const int bq = blockIdx.y;
+  a.q += (size_t)bq * a.rows * a.ldq;                       // request-major Q rows
+  a.k += (size_t)bq * a.kv_bstride;
+  a.v += (size_t)bq * a.kv_bstride;
+  a.part += (size_t)bq * a.nchunks * a.rows_pad * ATT_HD;
+  a.lse += (size_t)bq * a.nchunks * a.rows_pad;
 
   PI0_PROBE(0);
   // ---- stage K, V, Q with coalesced loads. The buffer resources end at the last
@@ -193,7 +211,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
       const int id = t + 256 * j, grow = q0 + (id >> 6), col = (id & 63) * 4;
       if (grow < a.rows) {
         const bf16x4 pk = {f2bf(acc[j][0]), f2bf(acc[j][1]), f2bf(acc[j][2]), f2bf(acc[j][3])};
-        *reinterpret_cast<bf16x4*>(a.out + (size_t)grow * a.ldo + col) = pk;
+        *reinterpret_cast<bf16x4*>(a.out + (size_t)out_row(a, bq, grow) * a.ldo + col) = pk;
       }
     }
     return;
@@ -215,8 +233,11 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
 // (row (b*256 + t) / 64, columns 4*(t%64)..) over the chunks, in chunk order.
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   const int id = blockIdx.x * 256 + threadIdx.x;
-  const int row = id >> 6, col = (id & 63) * 4;
-  if (row >= a.rows) return;
+  const int grow = id >> 6, col = (id & 63) * 4;
+  if (grow >= a.rows * a.batch) return;
+  const int bq = grow / a.rows, row = grow - bq * a.rows;
+  a.part += (size_t)bq * a.nchunks * a.rows_pad * ATT_HD;
+  a.lse += (size_t)bq * a.nchunks * a.rows_pad;
   float lse_c[MAX_CHUNKS];
   f32x4 pv[MAX_CHUNKS];
 #pragma unroll
@@ -241,7 +262,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
   }
   const float winv = wsum > 0.f ? __builtin_amdgcn_rcpf(wsum) : 0.f;
   const bf16x4 pk = {f2bf(o4[0] * winv), f2bf(o4[1] * winv), f2bf(o4[2] * winv), f2bf(o4[3] * winv)};
-  *reinterpret_cast<bf16x4*>(a.out + (size_t)row * a.ldo + col) = pk;
+  *reinterpret_cast<bf16x4*>(a.out + (size_t)out_row(a, bq, row) * a.ldo + col) = pk;
 }
 
 }  // namespace pi0
@@ -252,21 +273,34 @@ static inline size_t round256(size_t v) { return (v + 255) / 256 * 256; }
 
 extern "C" {
 
-size_t pi0hip_attention_workspace_bytes(int rows, int keys) {
-  if (rows <= 0 || keys <= 0) return 0;
+size_t pi0hip_attention_batched_workspace_bytes(int rows, int keys, int batch) {
+  if (rows <= 0 || keys <= 0 || batch <= 0) return 0;
   const size_t nch = (size_t)(keys + ATT_CH - 1) / ATT_CH;
   const size_t nqt = (size_t)(rows + ATT_QT - 1) / ATT_QT;
   const size_t rows_pad = nqt * ATT_QT;
-  return round256(nch * rows_pad * sizeof(float)) + nch * rows_pad * ATT_HD * sizeof(float);
+  return round256((size_t)batch * nch * rows_pad * sizeof(float)) +
+         (size_t)batch * nch * rows_pad * ATT_HD * sizeof(float);
 }
 
-int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int ldkv, void* out,
-                     int ldo, int rows, int keys, int enc_len, int heads, int head_dim,
-                     void* ws, size_t ws_bytes, hipStream_t s) {
-  if (!q || !k || !v || !out || rows <= 0 || keys <= 0) return PI0HIP_ERR_ARG;
-  if (head_dim != ATT_HD || keys > MAX_CHUNKS * ATT_CH) return PI0HIP_ERR_SHAPE;
-  if (!ws || ws_bytes < pi0hip_attention_workspace_bytes(rows, keys)) return PI0HIP_ERR_WORKSPACE;
+size_t pi0hip_attention_workspace_bytes(int rows, int keys) {
+  return pi0hip_attention_batched_workspace_bytes(rows, keys, 1);
+}
+
+int pi0hip_attention_batched(const void* q, int ldq, const void* k, const void* v, int ldkv,
+                             long long kv_bstride, void* out, int ldo, int rows, int keys,
+                             int enc_len, int heads, int head_dim, int batch, void* ws,
+                             size_t ws_bytes, hipStream_t s) {
+  if (!q || !k || !v || !out || rows <= 0 || keys <= 0 || batch <= 0 || heads <= 0)
+    return PI0HIP_ERR_ARG;
+  if (head_dim != ATT_HD || keys > MAX_CHUNKS * ATT_CH || (batch > 1 && rows % heads))
+    return PI0HIP_ERR_SHAPE;
+  if (!ws || ws_bytes < pi0hip_attention_batched_workspace_bytes(rows, keys, batch))
+    return PI0HIP_ERR_WORKSPACE;
+  // with one key chunk the output is stored by the split launch itself, which must not
+  // overwrite query rows that other workgroups of a multi-request batch still read
+  if (batch > 1 && keys <= ATT_CH && out == q) return PI0HIP_ERR_ARG;
   AttnArgs a = {};
+  a.batch = batch; a.kv_bstride = kv_bstride;
   a.q = (const __bf16*)q; a.ldq = ldq;
   a.k = (const __bf16*)k; a.v = (const __bf16*)v; a.ldkv = ldkv;
   a.out = (__bf16*)out; a.ldo = ldo;
@@ -278,15 +312,23 @@ int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int l
   const int grid = nqt * a.nchunks;
   char* base = reinterpret_cast<char*>(ws);
   a.lse = reinterpret_cast<float*>(base);
-  base += round256((size_t)a.nchunks * a.rows_pad * sizeof(float));
+  base += round256((size_t)batch * a.nchunks * a.rows_pad * sizeof(float));
   a.part = reinterpret_cast<float*>(base);
   a.scale_log2 = 1.4426950408889634f / sqrtf((float)head_dim);
-  hipLaunchKernelGGL(attn_kernel, dim3(grid), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(attn_kernel, dim3(grid, batch), dim3(256), 0, s, a);
   if (a.nchunks > 1) {
     if (hipError_t e = hipGetLastError()) return (int)e;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((rows * 64 + 255) / 256), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((batch * rows * 64 + 255) / 256), dim3(256), 0, s,
+                       a);
   }
   return (int)hipGetLastError();
+}
+
+int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int ldkv, void* out,
+                     int ldo, int rows, int keys, int enc_len, int heads, int head_dim,
+                     void* ws, size_t ws_bytes, hipStream_t s) {
+  return pi0hip_attention_batched(q, ldq, k, v, ldkv, 0, out, ldo, rows, keys, enc_len, heads,
+                                  head_dim, 1, ws, ws_bytes, s);
 }
 
 }  // extern "C"

@@ -48,6 +48,8 @@ struct TileArgs {
   float* part;                          // TE_PARTIAL: [splitk][M][N] fp32
   const __bf16* res; int ldres, res_mod;  // TE_BIAS_RES residual (may alias out); res_mod 0 = row
   int n_valid;                          // output columns stored (<= N; the rest is padding)
+  int rows_per_batch;                   // TE_QKV_ROPE: prefix rows per request (RoPE position
+  long long kv_bstride;                 //   = row % rows_per_batch), cache stride per request
   int M, N, K;                          // N, K = the packed (padded) weight's shape
   int tiles_m, tiles_n, splitk, ksteps; // ksteps = 64-deep steps per split
   int heads, head_dim;
@@ -229,10 +231,11 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
     __bf16* dst;
     if constexpr (EPI == TE_QKV_ROPE) {
       const int hd = a.head_dim, qdim = a.heads * hd;
+      const int bq = grow / a.rows_per_batch, tq = grow - bq * a.rows_per_batch;
 #pragma unroll
       for (int q = 0; q < 8; ++q) v[q] = round_bf(v[q]);
       if (col < qdim + hd) {          // rotate the rounded pairs (2p, 2p + 1)
-        const bf16x8 rp = load8(a.rope + (size_t)grow * hd + (col % hd));
+        const bf16x8 rp = load8(a.rope + (size_t)tq * hd + (col % hd));
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
           const float cs_ = bf2f(rp[2 * p]), sn = bf2f(rp[2 * p + 1]);
@@ -241,9 +244,10 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
           v[2 * p + 1] = x1 * cs_ + x0 * sn;
         }
       }
+      const size_t kv = (size_t)bq * a.kv_bstride + (size_t)tq * a.ldkv;
       if (col < qdim) dst = a.out + (size_t)grow * qdim + col;
-      else if (col < qdim + hd) dst = a.out_k + (size_t)grow * a.ldkv + (col - qdim);
-      else dst = a.out_v + (size_t)grow * a.ldkv + (col - qdim - hd);
+      else if (col < qdim + hd) dst = a.out_k + kv + (col - qdim);
+      else dst = a.out_v + kv + (col - qdim - hd);
     } else {
       dst = a.out + (size_t)grow * a.ldo + col;
       if constexpr (EPI == TE_BIAS) {
@@ -409,8 +413,9 @@ struct EncAttnArgs {
   const __bf16* k; int ldk;
   const __bf16* vt; int ldvt;           // V^T [256][ldvt], keys zero-padded to a multiple of 32
   __bf16* out; int ldo;
-  int rows, keys;
+  int rows, keys;                       // per request (grid.y = requests)
   float scale_log2;
+  long long kv_bstride;                 // elements between two requests' K
 };
 
 // V [keys][ldv] -> V^T [256][ldvt], zero beyond `keys` (64 x 64 tiles through LDS).
@@ -418,9 +423,11 @@ struct EncAttnArgs {
 // {0-3, 8-11, 4-7, 12-15}, so one lane's 8 keys are one 16-byte load.
 __global__ __launch_bounds__(256) void transpose_v_kernel(const __bf16* __restrict__ v, int ldv,
                                                           __bf16* __restrict__ vt, int ldvt,
-                                                          int keys) {
+                                                          int keys, long long v_bstride) {
   __shared__ __bf16 tile[64][66];
   const int k0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
+  v += (size_t)blockIdx.z * v_bstride;
+  vt += (size_t)blockIdx.z * EA_HD * ldvt;
   const int t = threadIdx.x;
   for (int i = t; i < 64 * 64; i += 256) {
     const int kr = i >> 6, dc = i & 63;
@@ -442,6 +449,13 @@ __global__ __launch_bounds__(256, 1) void enc_attn_kernel(EncAttnArgs a) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int r = lane & 31, h = lane >> 5;
   const int q0 = blockIdx.x * 32;
+  {                                     // request blockIdx.y: its rows, K and V^T
+    const int bq = blockIdx.y;
+    a.q += (size_t)bq * a.rows * a.ldq;
+    a.out += (size_t)bq * a.rows * a.ldo;
+    a.k += (size_t)bq * a.kv_bstride;
+    a.vt += (size_t)bq * EA_HD * a.ldvt;
+  }
 
   // Q^T fragments (B operand, 16 d each; lane holds Q[q0 + r][16 kk + 8 h .. + 7]) are
   // shared by the 4 waves: staged once in LDS (in the merge buffer's space)
@@ -713,6 +727,28 @@ __global__ __launch_bounds__(64) void vision_attn_kernel(VisAttnArgs a) {
     }
 }
 
+
+// Prompt embedding (the reference takes precomputed embeddings,
+// spec.py:46): out[b * rows_per_batch + row0 + j] = bf16(table[ids[b][j]] * scale).
+__global__ __launch_bounds__(256) void embed_tokens_kernel(const int* __restrict__ ids, int n_tok,
+                                                           const __bf16* __restrict__ table,
+                                                           int vocab, int dim, float scale,
+                                                           __bf16* __restrict__ out, int ldo,
+                                                           int row0, int rows_per_batch,
+                                                           int total) {
+  const int per_row = dim >> 3;
+  const int id = blockIdx.x * 256 + threadIdx.x;
+  if (id >= total * per_row) return;
+  const int tok = id / per_row, c = (id - tok * per_row) * 8;
+  const int b = tok / n_tok, j = tok - b * n_tok;
+  const int v = min(max(ids[tok], 0), vocab - 1);      // out-of-range ids clamp (checked on host)
+  const bf16x8 e = load8(table + (size_t)v * dim + c);
+  bf16x8 o;
+#pragma unroll
+  for (int q = 0; q < 8; ++q) o[q] = f2bf(bf2f(e[q]) * scale);
+  *reinterpret_cast<bf16x8*>(out + ((size_t)b * rows_per_batch + row0 + j) * ldo + c) = o;
+}
+
 }  // namespace pi0
 
 using namespace pi0;
@@ -752,7 +788,7 @@ static TileArgs tile_args(const void* x, int ldx, const void* w, void* out, int 
   TileArgs a = {};
   a.a = (const __bf16*)x; a.lda = ldx; a.w0 = (const __bf16*)w;
   a.out = (__bf16*)out; a.ldo = ldo;
-  a.M = M; a.N = N; a.K = K; a.splitk = 1; a.n_valid = N;
+  a.M = M; a.N = N; a.K = K; a.splitk = 1; a.n_valid = N; a.rows_per_batch = M;
   return a;
 }
 
@@ -835,14 +871,25 @@ int pi0hip_tile_gated_ffn(const void* x, int ldx, const void* gate_packed, const
 int pi0hip_tile_qkv_rope(const void* x, int ldx, const void* w_packed, const void* rope, void* q,
                          void* k, void* v, int ldkv, int M, int K, int heads, int head_dim,
                          hipStream_t s) {
-  if (!x || !w_packed || !rope || !q || !k || !v || M <= 0 || K <= 0 || heads <= 0)
+  return pi0hip_tile_qkv_rope_batched(x, ldx, w_packed, rope, q, k, v, ldkv, 0, M, M, K, heads,
+                                      head_dim, s);
+}
+
+int pi0hip_tile_qkv_rope_batched(const void* x, int ldx, const void* w_packed, const void* rope,
+                                 void* q, void* k, void* v, int ldkv, long long kv_bstride,
+                                 int rows_per_batch, int M, int K, int heads, int head_dim,
+                                 hipStream_t s) {
+  if (!x || !w_packed || !rope || !q || !k || !v || M <= 0 || K <= 0 || heads <= 0 ||
+      rows_per_batch <= 0)
     return PI0HIP_ERR_ARG;
+  if (M % rows_per_batch || (kv_bstride & 7)) return PI0HIP_ERR_SHAPE;
   if (head_dim % 16 || misaligned(x, ldx) || misaligned(q, 0) || misaligned(k, ldkv) ||
       misaligned(v, ldkv) || misaligned(rope, head_dim))
     return PI0HIP_ERR_SHAPE;
   TileArgs a = tile_args(x, ldx, w_packed, q, heads * head_dim, M, (heads + 2) * head_dim, K);
   a.out_k = (__bf16*)k; a.out_v = (__bf16*)v; a.ldkv = ldkv;
   a.rope = (const __bf16*)rope; a.heads = heads; a.head_dim = head_dim;
+  a.rows_per_batch = rows_per_batch; a.kv_bstride = kv_bstride;
   return launch_tile_auto<64, 32, 8, TE_QKV_ROPE, false>(a, s);
 }
 
@@ -857,23 +904,36 @@ int pi0hip_layer_norm(const void* x, int ldx, const void* w, const void* b, void
 
 static inline size_t round256_(size_t v) { return (v + 255) / 256 * 256; }
 
-size_t pi0hip_encoder_attention_workspace_bytes(int keys) {
-  if (keys <= 0) return 0;
+size_t pi0hip_encoder_attention_batched_workspace_bytes(int keys, int batch) {
+  if (keys <= 0 || batch <= 0) return 0;
   const size_t ldvt = (size_t)(keys + 63) / 64 * 64;
-  return round256_((size_t)EA_HD * ldvt * sizeof(__bf16));
+  return round256_((size_t)batch * EA_HD * ldvt * sizeof(__bf16));
+}
+
+size_t pi0hip_encoder_attention_workspace_bytes(int keys) {
+  return pi0hip_encoder_attention_batched_workspace_bytes(keys, 1);
 }
 
 int pi0hip_encoder_attention(const void* q, int ldq, const void* k, const void* v, int ldkv,
                              void* out, int ldo, int rows, int keys, int head_dim, float scale,
                              void* ws, size_t ws_bytes, hipStream_t s) {
-  if (!q || !k || !v || !out || rows <= 0 || keys <= 0) return PI0HIP_ERR_ARG;
+  return pi0hip_encoder_attention_batched(q, ldq, k, v, ldkv, 0, out, ldo, rows, keys, head_dim,
+                                          scale, 1, ws, ws_bytes, s);
+}
+
+int pi0hip_encoder_attention_batched(const void* q, int ldq, const void* k, const void* v,
+                                     int ldkv, long long kv_bstride, void* out, int ldo, int rows,
+                                     int keys, int head_dim, float scale, int batch, void* ws,
+                                     size_t ws_bytes, hipStream_t s) {
+  if (!q || !k || !v || !out || rows <= 0 || keys <= 0 || batch <= 0) return PI0HIP_ERR_ARG;
   if (head_dim != EA_HD || misaligned(q, ldq) || misaligned(k, ldkv) || (ldo & 3) ||
-      (reinterpret_cast<uintptr_t>(out) & 7))
+      (reinterpret_cast<uintptr_t>(out) & 7) || (kv_bstride & 7))
     return PI0HIP_ERR_SHAPE;
-  if (!ws || ws_bytes < pi0hip_encoder_attention_workspace_bytes(keys)) return PI0HIP_ERR_WORKSPACE;
+  if (!ws || ws_bytes < pi0hip_encoder_attention_batched_workspace_bytes(keys, batch))
+    return PI0HIP_ERR_WORKSPACE;
   const int ldvt = (keys + 63) / 64 * 64;
-  hipLaunchKernelGGL(transpose_v_kernel, dim3(ldvt / 64, EA_HD / 64), dim3(256), 0, s,
-                     (const __bf16*)v, ldkv, (__bf16*)ws, ldvt, keys);
+  hipLaunchKernelGGL(transpose_v_kernel, dim3(ldvt / 64, EA_HD / 64, batch), dim3(256), 0, s,
+                     (const __bf16*)v, ldkv, (__bf16*)ws, ldvt, keys, kv_bstride);
   if (hipError_t e = hipGetLastError()) return (int)e;
   EncAttnArgs a = {};
   a.q = (const __bf16*)q; a.ldq = ldq;
@@ -882,7 +942,8 @@ int pi0hip_encoder_attention(const void* q, int ldq, const void* k, const void* 
   a.out = (__bf16*)out; a.ldo = ldo;
   a.rows = rows; a.keys = keys;
   a.scale_log2 = 1.4426950408889634f * scale;
-  hipLaunchKernelGGL(enc_attn_kernel, dim3((rows + 31) / 32), dim3(256), 0, s, a);
+  a.kv_bstride = kv_bstride;
+  hipLaunchKernelGGL(enc_attn_kernel, dim3((rows + 31) / 32, batch), dim3(256), 0, s, a);
   return (int)hipGetLastError();
 }
 
@@ -949,6 +1010,20 @@ int pi0hip_vision_attention(const void* qkv, int ldqkv, void* out, int ldo, int 
   a.heads = heads; a.dim = dim;
   a.scale_log2 = 1.4426950408889634f * scale;
   hipLaunchKernelGGL(vision_attn_kernel, dim3(VA_TOK / 32, heads, views), dim3(64), 0, s, a);
+  return (int)hipGetLastError();
+}
+
+int pi0hip_embed_tokens(const int* ids, int n_tok, int batch, const void* table, int vocab, int dim,
+                        float scale, void* out, int ldo, int row0, int rows_per_batch,
+                        hipStream_t s) {
+  if (!ids || !table || !out || n_tok <= 0 || batch <= 0 || vocab <= 0 || dim <= 0)
+    return PI0HIP_ERR_ARG;
+  if (dim % 8 || misaligned(out, ldo) || misaligned(table, dim) || row0 + n_tok > rows_per_batch)
+    return PI0HIP_ERR_SHAPE;
+  const int total = n_tok * batch;
+  hipLaunchKernelGGL(embed_tokens_kernel, dim3((total * (dim / 8) + 255) / 256), dim3(256), 0, s,
+                     ids, n_tok, (const __bf16*)table, vocab, dim, scale, (__bf16*)out, ldo, row0,
+                     rows_per_batch, total);
   return (int)hipGetLastError();
 }
 

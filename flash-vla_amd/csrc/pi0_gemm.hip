@@ -37,6 +37,8 @@ struct GemmArgs {
   __bf16* norm_factor;
   float* ws;
   int M, N, K, splitk, heads, head_dim;
+  int batch;              // EPI_QKV_ROPE: requests stacked "states first" (see gemm_epilogue)
+  long long kv_bstride;   // EPI_QKV_ROPE: elements between two requests' K / V caches
   float* out_f32;  // EPI_RMS_BIAS_RES: fp32 residual / destination instead of `out`
 };
 
@@ -88,12 +90,21 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int row, int nt
 #pragma unroll
     for (int c = 0; c < 4; ++c) o[c] = gelu_tanh(v0[c] * f) * (v1[c] * f);
   } else if constexpr (EPI == EPI_QKV_ROPE) {
+    // Row order of a batch of B requests: the B state tokens first, then the B x T action
+    // tokens request by request (for B = 1: state, actions). Token t of request b takes
+    // RoPE position t, Q row b (T + 1) + t (request-major) and cache row t of request b.
     const int hd = a.head_dim, qdim = a.heads * hd;
+    const int T = a.M / a.batch - 1;
+    int b = 0, t = row;
+    if (a.batch > 1) {
+      if (row < a.batch) { b = row; t = 0; }
+      else { b = (row - a.batch) / T; t = 1 + (row - a.batch) - b * T; }
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) o[c] = v0[c] * f;
     if (n < qdim + hd) {
       const int rj = n % hd;
-      const __bf16* rp = a.rope + (size_t)row * hd + rj;
+      const __bf16* rp = a.rope + (size_t)t * hd + rj;
 #pragma unroll
       for (int p = 0; p < 4; p += 2) {
         const float cs = bf2f(rp[p]), sn = bf2f(rp[p + 1]);
@@ -103,9 +114,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int row, int nt
       }
     }
     __bf16* dst;
-    if (n < qdim) dst = a.out + (size_t)row * qdim + n;
-    else if (n < qdim + hd) dst = a.out_k + (size_t)row * a.ldkv + (n - qdim);
-    else dst = a.out_v + (size_t)row * a.ldkv + (n - qdim - hd);
+    const size_t kv = (size_t)b * a.kv_bstride + (size_t)t * a.ldkv;
+    if (n < qdim) dst = a.out + ((size_t)b * (T + 1) + t) * qdim + n;
+    else if (n < qdim + hd) dst = a.out_k + kv + (n - qdim);
+    else dst = a.out_v + kv + (n - qdim - hd);
     bf16x4 pk = {f2bf(o[0]), f2bf(o[1]), f2bf(o[2]), f2bf(o[3])};
     *reinterpret_cast<bf16x4*>(dst) = pk;
     if (a.norm_factor && nt == 0 && nf_writer) a.norm_factor[row] = f2bf(f);
@@ -354,6 +366,7 @@ static int setup_ws(GemmArgs& a, void* ws, size_t ws_bytes, int dual) {
 static GemmArgs base_args(const void* x, int ldx, const void* w, void* out, int ldo,
                           int M, int N, int K, int splitk) {
   GemmArgs a = {};
+  a.batch = 1;
   a.x = (const __bf16*)x; a.ldx = ldx; a.w0 = (const __bf16*)w;
   a.out = (__bf16*)out; a.ldo = ldo;
   a.M = M; a.N = N; a.K = K; a.splitk = splitk;
@@ -412,16 +425,34 @@ int pi0hip_rms_linear_bias_residual_f32(const void* x, int ldx, const void* wp, 
   return launch_gemm<EPI_RMS_BIAS_RES, false>(a, s);
 }
 
-int pi0hip_norm_qkv_rope(const void* x, int ldx, const void* wp, const void* rope, void* q,
-                         void* k, void* v, int ldkv, void* norm_factor, int M, int K,
-                         int heads, int head_dim, hipStream_t s) {
-  if (!x || !wp || !rope || !q || !k || !v) return PI0HIP_ERR_ARG;
-  if (head_dim % 16 || heads <= 0) return PI0HIP_ERR_SHAPE;
+int pi0hip_norm_qkv_rope_batched(const void* x, int ldx, const void* wp, const void* rope, void* q,
+                                 void* k, void* v, int ldkv, long long kv_bstride,
+                                 void* norm_factor, int M, int K, int heads, int head_dim,
+                                 int batch, hipStream_t s) {
+  if (!x || !wp || !rope || !q || !k || !v || batch <= 0 || M <= 0) return PI0HIP_ERR_ARG;
+  if (head_dim % 16 || heads <= 0 || M % batch || M / batch < 2) return PI0HIP_ERR_SHAPE;
   GemmArgs a = base_args(x, ldx, wp, q, heads * head_dim, M, (heads + 2) * head_dim, K, 1);
   a.out_k = (__bf16*)k; a.out_v = (__bf16*)v; a.ldkv = ldkv;
   a.rope = (const __bf16*)rope; a.norm_factor = (__bf16*)norm_factor;
   a.heads = heads; a.head_dim = head_dim;
+  a.batch = batch; a.kv_bstride = kv_bstride;
   return launch_gemm<EPI_QKV_ROPE, false>(a, s);
+}
+
+int pi0hip_norm_qkv_rope(const void* x, int ldx, const void* wp, const void* rope, void* q,
+                         void* k, void* v, int ldkv, void* norm_factor, int M, int K,
+                         int heads, int head_dim, hipStream_t s) {
+  if (M == 1) {     // a lone state token: one request of one row
+    if (!x || !wp || !rope || !q || !k || !v) return PI0HIP_ERR_ARG;
+    if (head_dim % 16 || heads <= 0) return PI0HIP_ERR_SHAPE;
+    GemmArgs a = base_args(x, ldx, wp, q, heads * head_dim, M, (heads + 2) * head_dim, K, 1);
+    a.out_k = (__bf16*)k; a.out_v = (__bf16*)v; a.ldkv = ldkv;
+    a.rope = (const __bf16*)rope; a.norm_factor = (__bf16*)norm_factor;
+    a.heads = heads; a.head_dim = head_dim;
+    return launch_gemm<EPI_QKV_ROPE, false>(a, s);
+  }
+  return pi0hip_norm_qkv_rope_batched(x, ldx, wp, rope, q, k, v, ldkv, 0, norm_factor, M, K, heads,
+                                      head_dim, 1, s);
 }
 
 int pi0hip_norm_gated_ffn(const void* x, int ldx, const void* gate_p, const void* up_p,

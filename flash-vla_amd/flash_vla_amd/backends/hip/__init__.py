@@ -15,7 +15,8 @@ from .wrappers import prepare_weights, use_pool
 ALL_WRAPPERS = {**vision_wrappers.VISION_WRAPPERS, **encoder_wrappers.ENCODER_WRAPPERS,
                 **wrappers.ALL_WRAPPERS,
                 "vision_attention": vision_wrappers.vision_attention,
-                "encoder_attention": encoder_wrappers.encoder_attention}
+                "encoder_attention": encoder_wrappers.encoder_attention,
+                "embed_prompt": encoder_wrappers.embed_prompt}
 FUSED_WRAPPERS = dict(fused_wrappers.FUSED_WRAPPERS)
 
 __all__ = ["ALL_WRAPPERS", "FUSED_WRAPPERS", "prepare_weights", "use_pool", "wrappers",

@@ -35,6 +35,20 @@ PROTOTYPES = {
     "pi0hip_attention_workspace_bytes": (c_size_t, [c_int, c_int]),
     "pi0hip_attention": (c_int, [P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int, c_int,
                                  c_int, P, c_size_t, P]),
+    # batched (config 5)
+    "pi0hip_norm_qkv_rope_batched": (c_int, [P, c_int, P, P, P, P, P, c_int, ctypes.c_longlong, P,
+                                             c_int, c_int, c_int, c_int, c_int, P]),
+    "pi0hip_attention_batched_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "pi0hip_attention_batched": (c_int, [P, c_int, P, P, c_int, ctypes.c_longlong, P, c_int, c_int,
+                                         c_int, c_int, c_int, c_int, c_int, P, c_size_t, P]),
+    "pi0hip_tile_qkv_rope_batched": (c_int, [P, c_int, P, P, P, P, P, c_int, ctypes.c_longlong,
+                                             c_int, c_int, c_int, c_int, c_int, P]),
+    "pi0hip_encoder_attention_batched_workspace_bytes": (c_size_t, [c_int, c_int]),
+    "pi0hip_encoder_attention_batched": (c_int, [P, c_int, P, P, c_int, ctypes.c_longlong, P, c_int,
+                                                 c_int, c_int, c_int, c_float, c_int, P, c_size_t,
+                                                 P]),
+    "pi0hip_embed_tokens": (c_int, [P, c_int, c_int, P, c_int, c_int, c_float, P, c_int, c_int,
+                                    c_int, P]),
     # prefix encoder
     "pi0hip_pack_weight32": (c_int, [P, P, c_int, c_int, c_int, P]),
     "pi0hip_pack_weight32_padded": (c_int, [P, P, c_int, c_int, c_int, c_int, c_int, P]),

@@ -39,22 +39,29 @@ def encoder_projector(x, norm_w, norm_b, proj_w, proj_b, out, x_norm):
 
 
 def encoder_norm_qkv_rope(x, weight_qkv, rope, Q, K, V, x_norm):
-    """RMSNorm into x_norm, QKV projection, RoPE on the rounded values, scatter (wrappers.py:347-363)."""
-    _check(x, "x", 2); _check(x_norm, "x_norm", 2); _check(rope, "rope", 2)
-    _check(Q, "Q", 2); _check(K, "K", 2); _check(V, "V", 2)
+    """RMSNorm into x_norm, QKV projection, RoPE on the rounded values, scatter (wrappers.py:347-363).
+
+    Batched form (config 5): K / V are [requests, L, head_dim] views of the per-request
+    caches and x holds the requests' L prefix rows one request after another."""
+    _check(x, "x", 2); _check(x_norm, "x_norm", 2); _check(rope, "rope", 2); _check(Q, "Q", 2)
+    batch = K.shape[0] if K.dim() == 3 else 1
+    K2, V2 = (K[0], V[0]) if K.dim() == 3 else (K, V)
+    _check(K2, "K", 2); _check(V2, "V", 2)
     M, Kdim = x.shape
-    head_dim = V.shape[1]
+    head_dim = V2.shape[1]
     heads = Q.shape[0] // M
-    if (Q.shape != (M * heads, head_dim) or not Q.is_contiguous() or K.shape != (M, head_dim)
-            or V.shape != (M, head_dim) or K.stride(0) != V.stride(0)
+    L = K2.shape[0]
+    if (Q.shape != (M * heads, head_dim) or not Q.is_contiguous() or M != batch * L
+            or V.shape != K.shape or K2.stride(0) != V2.stride(0) or K.stride() != V.stride()
             or weight_qkv.shape != (Kdim, (heads + 2) * head_dim)
-            or rope.shape != (M, head_dim) or not rope.is_contiguous()
+            or rope.shape[0] < L or rope.shape[1] != head_dim or not rope.is_contiguous()
             or x_norm.shape[0] < M or x_norm.shape[1] != Kdim):
         raise ValueError("encoder_norm_qkv_rope: shape mismatch")
     _abi.call("pi0hip_rms_norm", _ptr(x), x.stride(0), _ptr(x_norm), x_norm.stride(0), M, Kdim,
               _stream())
-    _abi.call("pi0hip_tile_qkv_rope", _ptr(x_norm), x_norm.stride(0), packed_weight_ptr(weight_qkv, 32),
-              _ptr(rope), _ptr(Q), _ptr(K), _ptr(V), K.stride(0), M, Kdim, heads, head_dim,
+    _abi.call("pi0hip_tile_qkv_rope_batched", _ptr(x_norm), x_norm.stride(0),
+              packed_weight_ptr(weight_qkv, 32), _ptr(rope), _ptr(Q), _ptr(K2), _ptr(V2),
+              K2.stride(0), K.stride(0) if batch > 1 else 0, L, M, Kdim, heads, head_dim,
               _stream())
 
 
@@ -101,20 +108,43 @@ def encoder_ffn_down_residual(x, weight, out):
 
 def encoder_attention(Q, K, V, scale):
     """softmax(scale * Q K^T) V over all keys, one shared KV head; returns [M, heads * head_dim]
-    (kernels/attention.py:29-34). The result lives in a pool buffer reused by the next call."""
-    _check(Q, "Q", 2); _check(K, "K", 2); _check(V, "V", 2)
+    (kernels/attention.py:29-34). Batched form: K / V [requests, L, head_dim], Q the
+    requests' rows one after another. The result lives in a pool buffer reused by the
+    next call."""
+    _check(Q, "Q", 2)
+    batch = K.shape[0] if K.dim() == 3 else 1
+    K2, V2 = (K[0], V[0]) if K.dim() == 3 else (K, V)
+    _check(K2, "K", 2); _check(V2, "V", 2)
     rows, head_dim = Q.shape
-    keys = K.shape[0]
-    if V.shape != K.shape or K.shape[1] != head_dim or K.stride(0) != V.stride(0):
+    keys = K2.shape[0]
+    if (V.shape != K.shape or K2.shape[1] != head_dim or K2.stride(0) != V2.stride(0)
+            or K.stride() != V.stride() or rows % batch):
         raise ValueError("encoder_attention: shape mismatch")
     out = scratch("encoder_attn_out", (rows, head_dim), Q.dtype, Q.device)
-    nbytes = _abi.lib().pi0hip_encoder_attention_workspace_bytes(keys)
+    nbytes = _abi.lib().pi0hip_encoder_attention_batched_workspace_bytes(keys, batch)
     ws = scratch("encoder_attn_ws", (nbytes,), torch.uint8, Q.device)
-    _abi.call("pi0hip_encoder_attention", _ptr(Q), Q.stride(0), _ptr(K), _ptr(V), K.stride(0),
-              _ptr(out), out.stride(0), rows, keys, head_dim, float(scale), ws.data_ptr(), nbytes,
+    _abi.call("pi0hip_encoder_attention_batched", _ptr(Q), Q.stride(0), _ptr(K2), _ptr(V2),
+              K2.stride(0), K.stride(0) if batch > 1 else 0, _ptr(out), out.stride(0),
+              rows // batch, keys, head_dim, float(scale), batch, ws.data_ptr(), nbytes,
               _stream())
     width = 2048 if (rows * head_dim) % 2048 == 0 else head_dim
     return out.view(-1, width)
+
+
+def embed_prompt(token_ids, table, out, row0, rows_per_request, scale):
+    """Prompt token embedding, scaled (the reference takes precomputed
+    `language_embeds`, spec.py:46): out[b * rows_per_request + row0 + j] =
+    bf16(table[token_ids[b, j]] * scale)."""
+    if token_ids.dtype != torch.int32 or not token_ids.is_cuda or not token_ids.is_contiguous():
+        raise TypeError("token_ids must be a contiguous int32 GPU tensor")
+    _check(table, "table", 2); _check(out, "out", 2)
+    batch, n_tok = token_ids.shape if token_ids.dim() == 2 else (1, token_ids.shape[0])
+    vocab, dim = table.shape
+    if out.shape[1] != dim or out.shape[0] < batch * rows_per_request:
+        raise ValueError("embed_prompt: shape mismatch")
+    _abi.call("pi0hip_embed_tokens", _ptr(token_ids), n_tok, batch, _ptr(table), vocab, dim,
+              float(scale), _ptr(out), out.stride(0), row0, rows_per_request, _stream())
+    return out
 
 
 ENCODER_WRAPPERS = {

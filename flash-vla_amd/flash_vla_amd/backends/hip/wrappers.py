@@ -161,11 +161,12 @@ def clear_packed_cache() -> None:
 
 
 def _splitk(M: int, N: int, K: int, target: int = 256) -> int:
-    """Split K across workgroups until the grid covers the 256 CUs (K per wave stays >= 32)."""
+    """Split K across workgroups until the grid covers the 256 CUs, and at least until each
+    wave's K range fits the kernel's unrolled widths (1..8 fragments of 32)."""
     tiles = ((M + 63) // 64) * (N // 16)
     kt = K // 32
     s = 1
-    while tiles * s < target and kt % (4 * s * 2) == 0:
+    while (tiles * s < target or kt // (4 * s) > 8) and kt % (4 * s * 2) == 0:
         s *= 2
     return s
 
@@ -182,13 +183,14 @@ def _gemm_ws(role: str, M: int, N: int, splitk: int, dual: int, device):
 # Decoder call sites (pipeline.py:92-135 calls these by name)
 # ---------------------------------------------------------------------------
 def decoder_state_proj(x, weight, bias, out):
-    """out = x @ weight + bias for the state token (wrappers.py:108-112)."""
+    """out = x @ weight + bias for the state token(s) (wrappers.py:108-112); x [32] or [B, 32]."""
     _check(x, "x"); _check(weight, "weight", 2); _check(bias, "bias", 1); _check(out, "out", 2)
     K, N = weight.shape
-    if x.numel() != K or out.shape != (1, N) or bias.shape != (N,):
+    B = out.shape[0]
+    if x.numel() != B * K or out.shape != (B, N) or bias.shape != (N,) or not x.is_contiguous():
         raise ValueError("decoder_state_proj: shape mismatch")
     _abi.call("pi0hip_small_linear", _ptr(x), K, _ptr(weight), _ptr(bias), _ptr(out),
-              out.stride(0), 1, N, K, 0, _stream())
+              out.stride(0), B, N, K, 0, _stream())
     return out
 
 
@@ -222,16 +224,23 @@ def decoder_action_mlp(x, weight, bias, out):
 
 
 def decoder_norm_qkv_rope(x, weight_qkv, rope, Q, K, V, norm_factor):
-    """RMS factor, QKV projection, RoPE, scatter into Q and the K/V cache rows (wrappers.py:131-144)."""
+    """RMS factor, QKV projection, RoPE, scatter into Q and the K/V cache rows (wrappers.py:131-144).
+
+    Batched form: K / V are [requests, T + 1, head_dim] views of the
+    per-request caches and x holds the requests' rows "states first" (the requests'
+    state tokens, then each request's actions)."""
     _check(x, "x", 2); _check(rope, "rope", 2); _check(Q, "Q", 2)
-    _check(K, "K", 2); _check(V, "V", 2)
+    batch = K.shape[0] if K.dim() == 3 else 1
+    K2, V2 = (K[0], V[0]) if K.dim() == 3 else (K, V)
+    _check(K2, "K", 2); _check(V2, "V", 2)
     M, Kdim = x.shape
-    head_dim = V.shape[1]
+    head_dim = V2.shape[1]
     heads = Q.shape[0] // M
-    if (Q.shape != (M * heads, head_dim) or not Q.is_contiguous() or K.shape != (M, head_dim)
-            or V.shape != (M, head_dim) or K.stride(0) != V.stride(0)
+    rows = K2.shape[0]
+    if (Q.shape != (M * heads, head_dim) or not Q.is_contiguous() or M != batch * rows
+            or V.shape != K.shape or K2.stride(0) != V2.stride(0) or K.stride() != V.stride()
             or weight_qkv.shape != (Kdim, (heads + 2) * head_dim)
-            or rope.shape != (M, head_dim) or not rope.is_contiguous()):
+            or rope.shape[0] < rows or rope.shape[1] != head_dim or not rope.is_contiguous()):
         raise ValueError("decoder_norm_qkv_rope: shape mismatch")
     nf = 0
     if norm_factor is not None:
@@ -240,24 +249,37 @@ def decoder_norm_qkv_rope(x, weight_qkv, rope, Q, K, V, norm_factor):
             raise ValueError("norm_factor too short")
         nf = _ptr(norm_factor)
     wp = packed_weight_ptr(weight_qkv)
-    _abi.call("pi0hip_norm_qkv_rope", _ptr(x), x.stride(0), wp, _ptr(rope), _ptr(Q), _ptr(K),
-              _ptr(V), K.stride(0), nf, M, Kdim, heads, head_dim, _stream())
+    if batch == 1:
+        _abi.call("pi0hip_norm_qkv_rope", _ptr(x), x.stride(0), wp, _ptr(rope), _ptr(Q), _ptr(K2),
+                  _ptr(V2), K2.stride(0), nf, M, Kdim, heads, head_dim, _stream())
+    else:
+        _abi.call("pi0hip_norm_qkv_rope_batched", _ptr(x), x.stride(0), wp, _ptr(rope), _ptr(Q),
+                  _ptr(K2), _ptr(V2), K2.stride(0), K.stride(0), nf, M, Kdim, heads, head_dim,
+                  batch, _stream())
 
 
 def decoder_attention(Q, K, V, scores, out, encoder_seq_len):
-    """Masked single-KV-head attention; `out` may be `Q`, `scores` is unused (fused_wrappers.py:88-115)."""
-    _check(Q, "Q", 2); _check(K, "K", 2); _check(V, "V", 2); _check(out, "out", 2)
+    """Masked single-KV-head attention; `out` may be `Q`, `scores` is unused (fused_wrappers.py:88-115).
+
+    Batched form: K / V are [requests, keys, head_dim]; Q holds each request's query rows
+    request-major and `out` receives them in the "states first" token order."""
+    _check(Q, "Q", 2); _check(out, "out", 2)
+    batch = K.shape[0] if K.dim() == 3 else 1
+    K2, V2 = (K[0], V[0]) if K.dim() == 3 else (K, V)
+    _check(K2, "K", 2); _check(V2, "V", 2)
     rows, head_dim = Q.shape
-    keys = K.shape[0]
-    if V.shape != K.shape or K.shape[1] != head_dim or out.shape != Q.shape \
-            or K.stride(0) != V.stride(0):
+    keys = K2.shape[0]
+    if (V.shape != K.shape or K2.shape[1] != head_dim or out.shape != Q.shape
+            or K2.stride(0) != V2.stride(0) or K.stride() != V.stride() or rows % batch):
         raise ValueError("decoder_attention: shape mismatch")
     lib = _abi.lib()
-    nbytes = lib.pi0hip_attention_workspace_bytes(rows, keys)
+    per = rows // batch
+    nbytes = lib.pi0hip_attention_batched_workspace_bytes(per, keys, batch)
     ws = scratch("attn_ws", (nbytes,), torch.uint8, Q.device)
-    _abi.call("pi0hip_attention", _ptr(Q), Q.stride(0), _ptr(K), _ptr(V), K.stride(0), _ptr(out),
-              out.stride(0), rows, keys, int(encoder_seq_len), DECODER_HEADS, head_dim,
-              ws.data_ptr(), nbytes, _stream())
+    _abi.call("pi0hip_attention_batched", _ptr(Q), Q.stride(0), _ptr(K2), _ptr(V2), K2.stride(0),
+              K.stride(0) if batch > 1 else 0, _ptr(out), out.stride(0), per, keys,
+              int(encoder_seq_len), DECODER_HEADS, head_dim, batch, ws.data_ptr(), nbytes,
+              _stream())
     return out
 
 

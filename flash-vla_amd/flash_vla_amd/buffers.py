@@ -35,28 +35,37 @@ def rope_table(seq_len: int, offset: int, head_dim: int, device) -> torch.Tensor
 def allocate_decoder_buffers(encoder_seq_len: int, chunk_size: int, device,
                              layers: int = DECODER_LAYERS, width: int = DECODER_WIDTH,
                              ffn: int = DECODER_FFN, heads: int = DECODER_HEADS,
-                             head_dim: int = HEAD_DIM, action_dim: int = 32) -> dict:
-    """Every persistent buffer the decoder loop touches (buffers.py:37-64, decoder part)."""
+                             head_dim: int = HEAD_DIM, action_dim: int = 32,
+                             batch: int = 1) -> dict:
+    """Every persistent buffer the decoder loop touches (buffers.py:37-64, decoder part).
+
+    batch > 1 (the reference is batch-1 only): B requests share
+    every GEMM; their rows are stacked "states first" (the B state tokens, then the
+    B x chunk action tokens), each request has its own K/V cache
+    (`encoder_K/V` [B, layers, cache_len, head_dim]), state is [B, 32] and the noise
+    [B * chunk, 32]."""
     bf16 = torch.bfloat16
     dec_len = chunk_size + 1
     cache_len = encoder_seq_len + dec_len
+    B = batch
 
     def buf(*shape, dtype=bf16):
         return torch.zeros(shape, dtype=dtype, device=device)
 
+    cache = (layers, cache_len, head_dim) if B == 1 else (B, layers, cache_len, head_dim)
     buffers = {
-        "observation_state_normalized": buf(action_dim),
-        "diffusion_noise": buf(chunk_size, action_dim),
-        "encoder_K": buf(layers, cache_len, head_dim),
-        "encoder_V": buf(layers, cache_len, head_dim),
+        "observation_state_normalized": buf(action_dim) if B == 1 else buf(B, action_dim),
+        "diffusion_noise": buf(B * chunk_size, action_dim),
+        "encoder_K": buf(*cache),
+        "encoder_V": buf(*cache),
         "decoder_rope_weights": buf(dec_len, head_dim),
-        "decoder_x": buf(dec_len, width),
-        "decoder_x_buf": buf(chunk_size, width),
-        "decoder_state_buf": buf(1, width),
-        "decoder_norm_factor_buf": buf(dec_len),
-        "decoder_q_buf": buf(dec_len * heads, head_dim),
-        "decoder_attn_buf": buf(dec_len * heads, cache_len),
-        "decoder_hidden": buf(dec_len, ffn),
+        "decoder_x": buf(B * dec_len, width),
+        "decoder_x_buf": buf(B * chunk_size, width),
+        "decoder_state_buf": buf(B, width),
+        "decoder_norm_factor_buf": buf(B * dec_len),
+        "decoder_q_buf": buf(B * dec_len * heads, head_dim),
+        "decoder_attn_buf": buf(1, 1),      # unused by the fused attention (kept for the schema)
+        "decoder_hidden": buf(B * dec_len, ffn),
     }
     buffers["decoder_rope_weights"].copy_(rope_table(dec_len, encoder_seq_len, head_dim, device))
     return buffers
@@ -66,8 +75,9 @@ def allocate_encoder_buffers(encoder_seq_len: int, device, buffers: dict | None 
                              layers: int = ENCODER_LAYERS, width: int = ENCODER_WIDTH,
                              ffn: int = ENCODER_FFN, heads: int = DECODER_HEADS,
                              head_dim: int = HEAD_DIM, cache_len: int | None = None,
-                             num_views: int = 3) -> dict:
-    """The encoder part of `buffers.py:37-64`; adds to `buffers` (sharing its K/V cache)."""
+                             num_views: int = 3, batch: int = 1) -> dict:
+    """The encoder part of `buffers.py:37-64`; adds to `buffers` (sharing its K/V cache).
+    With batch B the B prefixes are stacked: encoder_x [B * encoder_seq_len, width]."""
     bf16 = torch.bfloat16
     buffers = {} if buffers is None else buffers
     if cache_len is None:
@@ -76,42 +86,45 @@ def allocate_encoder_buffers(encoder_seq_len: int, device, buffers: dict | None 
     def buf(*shape):
         return torch.zeros(shape, dtype=bf16, device=device)
 
+    B = batch
     buffers.update({
         "encoder_rope_weights": buf(encoder_seq_len, head_dim),
-        "encoder_x": buf(encoder_seq_len, width),
-        "encoder_x_norm": buf(encoder_seq_len, width),
-        "encoder_Q": buf(encoder_seq_len * heads, head_dim),
-        "encoder_hidden": buf(encoder_seq_len, ffn),
-        "vision_x_norm": buf(num_views, 256, VISION_WIDTH),
+        "encoder_x": buf(B * encoder_seq_len, width),
+        "encoder_x_norm": buf(B * encoder_seq_len, width),
+        "encoder_Q": buf(B * encoder_seq_len * heads, head_dim),
+        "encoder_hidden": buf(B * encoder_seq_len, ffn),
+        "vision_x_norm": buf(B * num_views, 256, VISION_WIDTH),
     })
     if "encoder_K" not in buffers:
-        buffers["encoder_K"] = buf(layers, cache_len, head_dim)
-        buffers["encoder_V"] = buf(layers, cache_len, head_dim)
+        cache = (layers, cache_len, head_dim) if B == 1 else (B, layers, cache_len, head_dim)
+        buffers["encoder_K"] = buf(*cache)
+        buffers["encoder_V"] = buf(*cache)
     buffers["encoder_rope_weights"].copy_(rope_table(encoder_seq_len, 0, head_dim, device))
     return buffers
 
 
 def allocate_static_buffers(num_views: int, chunk_size: int, prompt_len: int, device,
-                            vision_layers: int | None = None) -> tuple[dict, int]:
+                            batch: int = 1) -> tuple[dict, int]:
     """Every persistent buffer of the full forward (buffers.py:25-64 of the reference):
     images, state, noise, vision, encoder and decoder buffers, the K/V cache sized for
-    prefix + decoder rows, and both RoPE tables. Returns (buffers, encoder_seq_len)."""
-    del vision_layers
+    prefix + decoder rows, and both RoPE tables. Returns (buffers, encoder_seq_len).
+    batch > 1 stacks B requests (images [B * views, 224, 224, 3])."""
     bf16 = torch.bfloat16
+    B = batch
     encoder_seq_len = num_views * 256 + prompt_len
-    buffers = allocate_decoder_buffers(encoder_seq_len, chunk_size, device)
+    buffers = allocate_decoder_buffers(encoder_seq_len, chunk_size, device, batch=B)
     cache_len = encoder_seq_len + chunk_size + 1
     allocate_encoder_buffers(encoder_seq_len, device, buffers=buffers, cache_len=cache_len,
-                             num_views=num_views)
+                             num_views=num_views, batch=B)
 
     def buf(*shape):
         return torch.zeros(shape, dtype=bf16, device=device)
 
     buffers.update({
-        "observation_images_normalized": buf(num_views, 224, 224, 3),
-        "vision_x": buf(num_views, 256, VISION_WIDTH),
-        "vision_x_norm": buf(num_views, 256, VISION_WIDTH),
-        "vision_QKV": buf(num_views, 256, 3 * VISION_WIDTH),
-        "vision_hidden": buf(num_views, 256, 4304),
+        "observation_images_normalized": buf(B * num_views, 224, 224, 3),
+        "vision_x": buf(B * num_views, 256, VISION_WIDTH),
+        "vision_x_norm": buf(B * num_views, 256, VISION_WIDTH),
+        "vision_QKV": buf(B * num_views, 256, 3 * VISION_WIDTH),
+        "vision_hidden": buf(B * num_views, 256, 4304),
     })
     return buffers, encoder_seq_len

@@ -202,7 +202,13 @@ class Pi0Inference:
                  steps: int = 10, layers: int = 18, fused: bool = True, device: str = "cuda",
                  backend: str = "hip", plan: dict | None = None, fp32_euler: bool = True,
                  vision_layers: int | None = None, encoder_layers: int | None = None,
-                 capture: bool = True, warmup: int = 3):
+                 capture: bool = True, warmup: int = 3, batch: int = 1, prompt_tokens: int = 0):
+        """batch > 1 and prompt_tokens > 0 are the BASELINE config-5 profile (not in the
+        reference, which is batch-1 with precomputed `language_embeds`): B independent
+        requests share every GEMM, and each request's prompt is `prompt_tokens` token ids
+        embedded from `checkpoint["embed_tokens"]` ([vocab, 2048]) and scaled by sqrt(2048)."""
+        self.batch = batch
+        self.prompt_tokens = prompt_tokens
         self.num_views = num_views
         self.chunk_size = chunk_size
         self.steps = steps
@@ -211,9 +217,12 @@ class Pi0Inference:
         self.encoder_layers = encoder_layers
         self.ops = op_table(fused, backend=backend, plan=plan)
         self.backend = BACKENDS[backend]
-        self.prompt_len = len(checkpoint["language_embeds"])
+        self.prompt_len = prompt_tokens if prompt_tokens else len(checkpoint["language_embeds"])
         bf16 = torch.bfloat16
         shapes = weight_shapes(self.prompt_len)
+        if prompt_tokens:
+            shapes.pop("language_embeds")
+            shapes["embed_tokens"] = tuple(checkpoint["embed_tokens"].shape)
         self.weights = {}
         for name, shape in shapes.items():
             src = checkpoint[name]
@@ -228,10 +237,13 @@ class Pi0Inference:
             self.weights[name].copy_(src)
         self.layers = min(self.layers, self.weights["decoder_attn_qkv_w"].shape[0])
         self.buffers, self.encoder_seq_len = allocate_static_buffers(
-            num_views, chunk_size, self.prompt_len, device)
+            num_views, chunk_size, self.prompt_len, device, batch=batch)
+        if prompt_tokens:
+            self.buffers["prompt_token_ids"] = torch.zeros(batch, prompt_tokens, dtype=torch.int32,
+                                                           device=device)
         if fp32_euler:
             self.buffers["diffusion_noise_f32"] = torch.zeros(
-                chunk_size, shapes["decoder_state_in_proj_w"][0], dtype=torch.float32,
+                batch * chunk_size, shapes["decoder_state_in_proj_w"][0], dtype=torch.float32,
                 device=device)
         self.pool = ScratchPool()
         self.graph = None
@@ -243,8 +255,13 @@ class Pi0Inference:
     def _run(self):
         """One full forward pass, in place on the static buffers (engine.py:58-65)."""
         b = self.buffers
-        if self.prompt_len:
-            b["encoder_x"][self.num_views * 256:].copy_(self.weights["language_embeds"])
+        L, v0 = self.encoder_seq_len, self.num_views * 256
+        if self.prompt_tokens:
+            self.ops.embed_prompt(b["prompt_token_ids"], self.weights["embed_tokens"],
+                                  b["encoder_x"], v0, L, float(self.weights["embed_tokens"].shape[1]) ** 0.5)
+        elif self.prompt_len:
+            for r in range(self.batch):
+                b["encoder_x"][r * L + v0:(r + 1) * L].copy_(self.weights["language_embeds"])
         if "diffusion_noise_f32" in b:
             b["diffusion_noise_f32"].copy_(b["diffusion_noise"])
         with self.backend.use_pool(self.pool):
@@ -272,11 +289,19 @@ class Pi0Inference:
         torch.cuda.synchronize()
         self.buffers["diffusion_noise"].copy_(saved)
 
-    def forward(self, images, state, noise):
-        """Copy inputs into the static buffers, replay, return the denoised chunk (engine.py:80-86)."""
-        self.buffers["observation_images_normalized"].copy_(images)
-        self.buffers["observation_state_normalized"].copy_(state)
-        self.buffers["diffusion_noise"].copy_(noise)
+    def forward(self, images, state, noise, token_ids=None):
+        """Copy inputs into the static buffers, replay, return the denoised chunk (engine.py:80-86).
+
+        Batched: images [B, views, 224, 224, 3], state [B, 32], noise [B, chunk, 32] (the
+        result is [B * chunk, 32]), token_ids [B, prompt_tokens] int32."""
+        b = self.buffers
+        b["observation_images_normalized"].copy_(images.reshape(b["observation_images_normalized"].shape))
+        b["observation_state_normalized"].copy_(state.reshape(b["observation_state_normalized"].shape))
+        b["diffusion_noise"].copy_(noise.reshape(b["diffusion_noise"].shape))
+        if self.prompt_tokens:
+            if token_ids is None:
+                raise ValueError("this engine embeds its prompt from token ids: pass token_ids")
+            b["prompt_token_ids"].copy_(token_ids.reshape(b["prompt_token_ids"].shape))
         if self.graph is not None:
             self.graph.replay()
         else:

@@ -15,6 +15,21 @@ from __future__ import annotations
 from .spec import HEAD_DIM
 
 
+def _batch(buffers) -> int:
+    """Requests in flight: the per-request caches are [B, layers, rows, head_dim] when B > 1."""
+    k = buffers["encoder_K"]
+    return k.shape[0] if k.dim() == 4 else 1
+
+
+def _layer_cache(buffers, name, i, rows=None):
+    """Layer i's K or V cache rows (`rows` a slice) for one request ([rows, hd]) or a batch
+    ([B, rows, hd])."""
+    c = buffers[name]
+    if c.dim() == 4:
+        return c[:, i] if rows is None else c[:, i, rows]
+    return c[i] if rows is None else c[i][rows]
+
+
 def vision_encoder(ops, weights, buffers, num_views, layers=None):
     """Patch-embed the images and run the SigLIP layers, in place on `vision_x`
     (pipeline.py:21-54). `ops.vision_attention` is the op-table form of the
@@ -57,27 +72,32 @@ def transformer_encoder(ops, weights, buffers, encoder_seq_len, layers=None, pro
     `ops.encoder_attention` is the op-table form of the function the
     reference pipeline calls directly (`kernels/attention.py:29-34`).
     """
+    B = _batch(buffers)
     if project:
-        ops.encoder_projector(
-            buffers["vision_x"],
-            weights["vision_final_norm_w"], weights["vision_final_norm_b"],
-            weights["encoder_multi_modal_projector_w"], weights["encoder_multi_modal_projector_b"],
-            buffers["encoder_x"], buffers["vision_x_norm"])
+        views = buffers["vision_x"].shape[0] // B
+        for b in range(B):                 # request b's vision rows open its prefix
+            ops.encoder_projector(
+                buffers["vision_x"][b * views:(b + 1) * views],
+                weights["vision_final_norm_w"], weights["vision_final_norm_b"],
+                weights["encoder_multi_modal_projector_w"],
+                weights["encoder_multi_modal_projector_b"],
+                buffers["encoder_x"][b * encoder_seq_len:(b + 1) * encoder_seq_len],
+                buffers["vision_x_norm"][b * views:(b + 1) * views])
 
     scale = HEAD_DIM ** -0.5
     if layers is None:
         layers = weights["encoder_attn_qkv_w"].shape[0]
+    prefix = slice(0, encoder_seq_len)
     for i in range(layers):
+        k_i = _layer_cache(buffers, "encoder_K", i, prefix)
+        v_i = _layer_cache(buffers, "encoder_V", i, prefix)
         ops.encoder_norm_qkv_rope(
             buffers["encoder_x"], weights["encoder_attn_qkv_w"][i],
-            buffers["encoder_rope_weights"], buffers["encoder_Q"],
-            buffers["encoder_K"][i, :encoder_seq_len], buffers["encoder_V"][i, :encoder_seq_len],
+            buffers["encoder_rope_weights"], buffers["encoder_Q"], k_i, v_i,
             buffers["encoder_x_norm"])
         if i == layers - 1:
             break
-        attn = ops.encoder_attention(
-            buffers["encoder_Q"], buffers["encoder_K"][i, :encoder_seq_len],
-            buffers["encoder_V"][i, :encoder_seq_len], scale)
+        attn = ops.encoder_attention(buffers["encoder_Q"], k_i, v_i, scale)
         ops.encoder_out_proj_residual(attn, weights["encoder_attn_o_w"][i], buffers["encoder_x"])
         ops.encoder_norm_gated_ffn(
             buffers["encoder_x"], weights["encoder_ffn_gate_w"][i], weights["encoder_ffn_up_w"][i],
@@ -87,29 +107,32 @@ def transformer_encoder(ops, weights, buffers, encoder_seq_len, layers=None, pro
 
 
 def transformer_decoder(ops, weights, buffers, encoder_seq_len, steps=10, layers=18):
+    B = _batch(buffers)
     ops.decoder_state_proj(
         buffers["observation_state_normalized"], weights["decoder_state_in_proj_w"],
         weights["decoder_state_in_proj_b"], buffers["decoder_state_buf"])
 
     noise = buffers.get("diffusion_noise_f32", buffers["diffusion_noise"])
+    dec_rows = slice(encoder_seq_len, None)
     for step in range(steps):
-        buffers["decoder_x"][:1].copy_(buffers["decoder_state_buf"])
+        buffers["decoder_x"][:B].copy_(buffers["decoder_state_buf"])
         ops.decoder_action_in_proj(
             noise, weights["decoder_action_fused_in_proj_w"],
             weights["decoder_action_fused_time_biases"][step % 10], buffers["decoder_x_buf"])
         ops.decoder_action_mlp(
             buffers["decoder_x_buf"], weights["decoder_action_mlp_w"],
-            weights["decoder_action_mlp_b"], buffers["decoder_x"][1:])
+            weights["decoder_action_mlp_b"], buffers["decoder_x"][B:])
 
         for i in range(layers):
             ops.decoder_norm_qkv_rope(
                 buffers["decoder_x"], weights["decoder_attn_qkv_w"][i],
                 buffers["decoder_rope_weights"], buffers["decoder_q_buf"],
-                buffers["encoder_K"][i][encoder_seq_len:],
-                buffers["encoder_V"][i][encoder_seq_len:],
+                _layer_cache(buffers, "encoder_K", i, dec_rows),
+                _layer_cache(buffers, "encoder_V", i, dec_rows),
                 buffers["decoder_norm_factor_buf"])
             ops.decoder_attention(
-                buffers["decoder_q_buf"], buffers["encoder_K"][i], buffers["encoder_V"][i],
+                buffers["decoder_q_buf"], _layer_cache(buffers, "encoder_K", i),
+                _layer_cache(buffers, "encoder_V", i),
                 buffers["decoder_attn_buf"], buffers["decoder_q_buf"], encoder_seq_len)
             ops.decoder_out_proj_residual(
                 buffers["decoder_q_buf"].view(buffers["decoder_x"].shape[0], -1), weights["decoder_attn_o_w"][i],
@@ -122,7 +145,7 @@ def transformer_decoder(ops, weights, buffers, encoder_seq_len, steps=10, layers
                 buffers["decoder_hidden"], weights["decoder_ffn_down_w"][i], buffers["decoder_x"])
 
         ops.decoder_action_out_proj(
-            buffers["decoder_x"][1:], weights["decoder_action_fused_out_proj_w"],
+            buffers["decoder_x"][B:], weights["decoder_action_fused_out_proj_w"],
             weights["decoder_action_fused_out_proj_b"], noise,
             buffers["decoder_norm_factor_buf"])
 

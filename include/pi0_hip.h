@@ -97,6 +97,30 @@ int pi0hip_norm_gated_ffn(const void* x, int ldx, const void* gate_packed, const
 /* Workspace for pi0hip_attention. */
 size_t pi0hip_attention_workspace_bytes(int rows, int keys);
 
+/* pi0hip_norm_qkv_rope for a batch of `batch` requests (the
+ * reference is batch-1 only): the M = batch x (T + 1) rows are ordered "states
+ * first" (the batch's state tokens, then each request's T action tokens); token t
+ * of request b uses RoPE row t, writes Q row b (T + 1) + t (request-major) and K / V
+ * row t of request b's cache at k / v + b * kv_bstride. batch = 1 is
+ * pi0hip_norm_qkv_rope. decoder_norm_qkv_rope wrappers.py:131-144 (batched). */
+int pi0hip_norm_qkv_rope_batched(const void* x, int ldx, const void* w_packed, const void* rope,
+                                 void* q, void* k, void* v, int ldkv, long long kv_bstride,
+                                 void* norm_factor, int M, int K, int heads, int head_dim,
+                                 int batch, hipStream_t s);
+
+/* Workspace of pi0hip_attention_batched (rows and keys per request). */
+size_t pi0hip_attention_batched_workspace_bytes(int rows, int keys, int batch);
+
+/* pi0hip_attention over `batch` requests: request b's `rows` request-major query rows
+ * start at q + b * rows * ldq and read its own cache at k / v + b * kv_bstride; the
+ * output rows are written back in the "states first" token order of
+ * pi0hip_norm_qkv_rope_batched (rows % heads == 0 when batch > 1). batch = 1 is
+ * pi0hip_attention. decoder_attention fused_wrappers.py:88-115 (batched). */
+int pi0hip_attention_batched(const void* q, int ldq, const void* k, const void* v, int ldkv,
+                             long long kv_bstride, void* out, int ldo, int rows, int keys,
+                             int enc_len, int heads, int head_dim, int batch, void* ws,
+                             size_t ws_bytes, hipStream_t s);
+
 /* out = softmax(mask(q k^T / sqrt(head_dim))) v over `keys` cache rows; flat
  * query row r = token * heads + head; rows r < heads keep keys j <= enc_len.
  * `out` may alias `q`. head_dim must be 256, keys <= 1024.
@@ -164,6 +188,33 @@ int pi0hip_tile_qkv_rope(const void* x, int ldx, const void* w_packed, const voi
  * kernels/base.py:405-447) */
 int pi0hip_layer_norm(const void* x, int ldx, const void* w, const void* b, void* out, int ldo,
                       int M, int K, float eps, hipStream_t s);
+
+/* pi0hip_tile_qkv_rope over requests of `rows_per_batch` prefix rows each: row r is
+ * position r % rows_per_batch of request r / rows_per_batch, whose K / V cache starts at
+ * k / v + request * kv_bstride. encoder_norm_qkv_rope (batched, config 5). */
+int pi0hip_tile_qkv_rope_batched(const void* x, int ldx, const void* w_packed, const void* rope,
+                                 void* q, void* k, void* v, int ldkv, long long kv_bstride,
+                                 int rows_per_batch, int M, int K, int heads, int head_dim,
+                                 hipStream_t s);
+
+/* Workspace of pi0hip_encoder_attention_batched. */
+size_t pi0hip_encoder_attention_batched_workspace_bytes(int keys, int batch);
+
+/* pi0hip_encoder_attention over `batch` requests: request b's `rows` query / output rows
+ * follow request b - 1's, its K / V start at k / v + b * kv_bstride.
+ * encoder_attention (batched, config 5). */
+int pi0hip_encoder_attention_batched(const void* q, int ldq, const void* k, const void* v,
+                                     int ldkv, long long kv_bstride, void* out, int ldo, int rows,
+                                     int keys, int head_dim, float scale, int batch, void* ws,
+                                     size_t ws_bytes, hipStream_t s);
+
+/* Prompt embedding: out[b * rows_per_batch + row0 + j] = bf16(table[ids[b * n_tok + j]] *
+ * scale) for a [vocab, dim] bf16 table and int32 ids (clamped to the vocabulary).
+ * No reference counterpart (it takes precomputed language_embeds, spec.py:46,
+ * engine.py:60); BASELINE config 5's 48-token prompt, scale sqrt(2048). */
+int pi0hip_embed_tokens(const int* ids, int n_tok, int batch, const void* table, int vocab, int dim,
+                        float scale, void* out, int ldo, int row0, int rows_per_batch,
+                        hipStream_t s);
 
 /* Workspace of pi0hip_encoder_attention: the transposed V (256 x keys rounded up to 64). */
 size_t pi0hip_encoder_attention_workspace_bytes(int keys);

@@ -66,7 +66,8 @@ def test_rejected_arguments_do_not_launch():
 ENCODER_OPS = {"encoder_projector", "encoder_norm_qkv_rope", "encoder_out_proj_residual",
                "encoder_norm_gated_ffn", "encoder_ffn_down_residual", "encoder_attention",
                "vision_patch_embed", "vision_norm_qkv", "vision_out_proj_residual",
-               "vision_norm_ffn_up", "vision_ffn_down_residual", "vision_attention"}
+               "vision_norm_ffn_up", "vision_ffn_down_residual", "vision_attention",
+               "embed_prompt"}
 
 
 def test_op_table_contract():
