@@ -318,6 +318,7 @@ static int launch_gemm(const GemmArgs& a, hipStream_t s) {
   return (int)hipGetLastError();
 }
 
+
 // W[batch][K][N] row-major -> packed B fragments, one thread per 16-byte fragment row.
 __global__ void pack_weight_kernel(const __bf16* __restrict__ w, __bf16* __restrict__ p,
                                    int K, int N, long long total_frags) {
