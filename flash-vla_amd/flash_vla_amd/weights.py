@@ -122,6 +122,24 @@ def interleave_rope_columns(weight: torch.Tensor, heads: int) -> torch.Tensor:
             .transpose(-1, -2).reshape(*lead, inputs, outputs))
 
 
+def fold_gemma_layers(p: dict) -> tuple:
+    """Fold the stacked Gemma layers of `p` into (qkv, o, gate, up, down), `[in, out]`.
+
+    Input-norm (1 + w) scales the rows of Q, K and V; the post-attention norm
+    scales the rows of gate and up (`openpi.py:86-90`); Q and K columns move
+    from half-split to adjacent-pair RoPE order (`openpi.py:101-125`).
+    """
+    heads = p["q_w"].shape[-1] // p["k_w"].shape[-1]
+    in_scale = (1.0 + p["input_norm_w"])[:, :, None]
+    post_scale = (1.0 + p["post_attn_norm_w"])[:, :, None]
+    qkv = torch.cat([
+        interleave_rope_columns(p["q_w"] * in_scale, heads),
+        interleave_rope_columns(p["k_w"] * in_scale, 1),
+        p["v_w"] * in_scale,
+    ], dim=-1)
+    return qkv, p["o_w"], p["gate_w"] * post_scale, p["up_w"] * post_scale, p["down_w"]
+
+
 def fold_decoder(p: dict, steps: int = NUM_STEPS, dt: float = EULER_DT,
                  out_dtype=torch.bfloat16) -> dict:
     """Fold unfolded parameters into the packed decoder schema.
@@ -132,15 +150,8 @@ def fold_decoder(p: dict, steps: int = NUM_STEPS, dt: float = EULER_DT,
     * final norm (1 + w) and the Euler dt fold into the output projection, so
       the step becomes `noise += b' + rms(x) @ W'`.
     """
-    heads = p["o_w"].shape[1] // p["k_w"].shape[2]
     width = p["time_mlp_out_w"].shape[0]
-    in_scale = (1.0 + p["input_norm_w"])[:, :, None]
-    post_scale = (1.0 + p["post_attn_norm_w"])[:, :, None]
-    qkv = torch.cat([
-        interleave_rope_columns(p["q_w"] * in_scale, heads),
-        interleave_rope_columns(p["k_w"] * in_scale, 1),
-        p["v_w"] * in_scale,
-    ], dim=-1)
+    qkv, o_w, gate, up, down = fold_gemma_layers(p)
     mix_a = p["time_mlp_in_w"][:width]
     mix_t = p["time_mlp_in_w"][width:]
     temb = sinusoidal_time_embedding(euler_times(steps, dt), width).to(p["action_in_w"].dtype)
@@ -152,10 +163,10 @@ def fold_decoder(p: dict, steps: int = NUM_STEPS, dt: float = EULER_DT,
         "decoder_action_fused_time_biases": time_biases,
         "decoder_action_mlp_w": p["time_mlp_out_w"], "decoder_action_mlp_b": p["time_mlp_out_b"],
         "decoder_attn_qkv_w": qkv,
-        "decoder_attn_o_w": p["o_w"],
-        "decoder_ffn_gate_w": p["gate_w"] * post_scale,
-        "decoder_ffn_up_w": p["up_w"] * post_scale,
-        "decoder_ffn_down_w": p["down_w"],
+        "decoder_attn_o_w": o_w,
+        "decoder_ffn_gate_w": gate,
+        "decoder_ffn_up_w": up,
+        "decoder_ffn_down_w": down,
         "decoder_action_fused_out_proj_w": dt * final * p["action_out_w"],
         "decoder_action_fused_out_proj_b": dt * p["action_out_b"],
     }
