@@ -783,6 +783,18 @@ static int launch_tile_auto(TileArgs a, hipStream_t s) {
   return PI0HIP_ERR_SHAPE;
 }
 
+// Pipeline depth preferring 4 (measured faster than 8 at K = 2048, M = 768), then 6 and 3.
+template <int BM, int WN, int EPI, bool DUAL, int OCC = 1>
+static int launch_tile_d4(TileArgs a, hipStream_t s) {
+  if (a.K % 64 || a.splitk < 1 || (a.K / 64) % a.splitk) return PI0HIP_ERR_SHAPE;
+  const int steps = a.K / 64 / a.splitk;
+  if (steps % 4 == 0) return launch_tile<BM, WN, 4, EPI, DUAL, OCC>(a, s);
+  if (steps % 6 == 0) return launch_tile<BM, WN, 6, EPI, DUAL, OCC>(a, s);
+  if (steps % 3 == 0) return launch_tile<BM, WN, 3, EPI, DUAL, OCC>(a, s);
+  if (steps % 2 == 0) return launch_tile<BM, WN, 2, EPI, DUAL, OCC>(a, s);
+  return PI0HIP_ERR_SHAPE;
+}
+
 static TileArgs tile_args(const void* x, int ldx, const void* w, void* out, int ldo, int M, int N,
                           int K) {
   TileArgs a = {};
@@ -839,8 +851,15 @@ int pi0hip_tile_linear(const void* x, int ldx, const void* w_packed, const void*
   if (misaligned(x, ldx) || misaligned(out, ldo) || misaligned(bias, 0)) return PI0HIP_ERR_SHAPE;
   TileArgs a = tile_args(x, ldx, w_packed, out, ldo, M, N, K);
   a.bias = (const __bf16*)bias;
-  return bias ? launch_tile_auto<64, 32, 8, TE_BIAS, false>(a, s)
-              : launch_tile_auto<64, 32, 8, TE_STORE, false>(a, s);
+  // 64-row tiles unless they overflow one round of the 256 CUs while 96-row tiles fit in
+  // one (vision QKV: 324 -> 216 workgroups); measured at M = 768.
+  const int steps = K / 64;
+  if (N % 128 == 0 && K % 64 == 0 && steps % 3 == 0 && ((M + 63) / 64) * (N / 128) > 256 &&
+      ((M + 95) / 96) * (N / 128) <= 256)
+    return bias ? launch_tile<96, 32, 3, TE_BIAS, false, 2>(a, s)
+                : launch_tile<96, 32, 3, TE_STORE, false, 2>(a, s);
+  return bias ? launch_tile_d4<64, 32, TE_BIAS, false>(a, s)
+              : launch_tile_d4<64, 32, TE_STORE, false>(a, s);
 }
 
 int pi0hip_tile_linear_residual(const void* x, int ldx, const void* w_packed, void* out, int ldo,
@@ -850,7 +869,7 @@ int pi0hip_tile_linear_residual(const void* x, int ldx, const void* w_packed, vo
   if (misaligned(x, ldx) || misaligned(out, ldo)) return PI0HIP_ERR_SHAPE;
   TileArgs a = tile_args(x, ldx, w_packed, out, ldo, M, N, K);
   a.splitk = splitk;
-  if (splitk == 1) return launch_tile_auto<64, 32, 8, TE_RES, false>(a, s);
+  if (splitk == 1) return launch_tile_d4<64, 32, TE_RES, false>(a, s);
   if (N % 4 || ldo % 4) return PI0HIP_ERR_SHAPE;
   if (!ws || ws_bytes < pi0hip_tile_workspace_bytes(M, N, splitk)) return PI0HIP_ERR_WORKSPACE;
   a.part = (float*)ws;
@@ -865,7 +884,7 @@ int pi0hip_tile_gated_ffn(const void* x, int ldx, const void* gate_packed, const
   if (misaligned(x, ldx) || misaligned(out, ldo)) return PI0HIP_ERR_SHAPE;
   TileArgs a = tile_args(x, ldx, gate_packed, out, ldo, M, N, K);
   a.w1 = (const __bf16*)up_packed;
-  return launch_tile_auto<96, 64, 2, TE_GATE, true, 2>(a, s);
+  return launch_tile_auto<128, 64, 2, TE_GATE, true, 2>(a, s);
 }
 
 int pi0hip_tile_qkv_rope(const void* x, int ldx, const void* w_packed, const void* rope, void* q,
@@ -890,7 +909,7 @@ int pi0hip_tile_qkv_rope_batched(const void* x, int ldx, const void* w_packed, c
   a.out_k = (__bf16*)k; a.out_v = (__bf16*)v; a.ldkv = ldkv;
   a.rope = (const __bf16*)rope; a.heads = heads; a.head_dim = head_dim;
   a.rows_per_batch = rows_per_batch; a.kv_bstride = kv_bstride;
-  return launch_tile_auto<64, 32, 8, TE_QKV_ROPE, false>(a, s);
+  return launch_tile_d4<64, 32, TE_QKV_ROPE, false>(a, s);
 }
 
 int pi0hip_layer_norm(const void* x, int ldx, const void* w, const void* b, void* out, int ldo,
@@ -972,6 +991,9 @@ int pi0hip_tile_linear_bias_gelu(const void* x, int ldx, const void* w_packed, c
   TileArgs a = tile_args(x, ldx, w_packed, out, ldo, M, N_pad, K_pad);
   a.n_valid = N;
   a.bias = (const __bf16*)bias;
+  // vision FFN up (K = 1152, N = 4352): 256-column tiles, two workgroups per CU
+  if (N_pad % 256 == 0 && K_pad % 192 == 0)
+    return launch_tile<64, 64, 3, TE_BIAS_GELU, false, 2>(a, s);
   return launch_tile_auto<64, 32, 8, TE_BIAS_GELU, false>(a, s);
 }
 
