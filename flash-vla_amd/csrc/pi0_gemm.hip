@@ -7,9 +7,9 @@
 // before the first MFMA so that the whole slice is in flight at once. The
 // activation rows come from L2 as MFMA A fragments. Waves split K; their
 // accumulators are summed in LDS. When the column tiles alone cannot fill the
-// chip (N = 1024), K is also split across workgroups and the last workgroup
-// to finish a tile (an atomic arrival counter, reset by that workgroup) sums
-// the fp32 partials in split order -- deterministic -- and runs the epilogue.
+// chip (N = 1024), K is also split across workgroups: they store fp32 partial
+// tiles and a second launch (splitk_reduce_kernel) sums them in split order --
+// deterministic -- and runs the epilogue.
 //
 // The epilogues are the decoder's fused call sites (reference file:line):
 //   EPI_BIAS        x@W + b                    decoder_action_mlp  (wrappers.py:123-128)
@@ -259,20 +259,29 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
 
 
 // Second pass of split-K: one workgroup per 64 x 16 output tile; thread t owns row
-// t/4, columns 4*(t%4)..; sums the splits in split order, then the epilogue.
-template <int EPI, bool DUAL>
+// t/4, columns 4*(t%4)..; sums the splits in split order, then the epilogue. SK is the
+// split count when it is known at compile time (exactly SK partial loads), 0 for any
+// count up to MAX_SPLITK. The residual of the EPI_RES call sites is loaded together
+// with the partials, so the kernel pays one memory round trip, not two.
+template <int EPI, bool DUAL, int SK>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a) {
   constexpr int ND = DUAL ? 2 : 1;
   constexpr bool RMS = uses_rms(EPI);
+  constexpr int NL = SK > 0 ? SK : MAX_SPLITK;
   const int t = threadIdx.x, lrow = t >> 2, c4 = (t & 3) * 4;
   const int nt = blockIdx.x, mb = blockIdx.y, ntiles = gridDim.x;
-  const int tile = mb * ntiles + nt, splitk = a.splitk;
+  const int tile = mb * ntiles + nt, splitk = SK > 0 ? SK : a.splitk;
   const size_t tiles = (size_t)gridDim.y * ntiles;
-  f32x4 q0[MAX_SPLITK], q1[MAX_SPLITK];
-  float qs[MAX_SPLITK];
+  const int row = mb * 64 + lrow;
+  bf16x4 res4 = {};
+  if constexpr (EPI == EPI_RES) {
+    if (row < a.M) res4 = *reinterpret_cast<const bf16x4*>(a.out + (size_t)row * a.ldo + nt * 16 + c4);
+  }
+  f32x4 q0[NL], q1[NL];
+  float qs[NL];
 #pragma unroll
-  for (int k = 0; k < MAX_SPLITK; ++k) {     // unconditional loads; extra ones are ignored
-    const int kk = min(k, splitk - 1);
+  for (int k = 0; k < NL; ++k) {     // unconditional loads; extra ones (SK = 0) are ignored
+    const int kk = SK > 0 ? k : min(k, splitk - 1);
     const float* p = a.ws + (((size_t)tile * splitk + kk) * 64 + lrow) * 16 * ND + c4;
     q0[k] = *reinterpret_cast<const f32x4*>(p);
     if constexpr (DUAL) q1[k] = *reinterpret_cast<const f32x4*>(p + 16);
@@ -280,8 +289,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a) {
   }
   float v0[4] = {0.f, 0.f, 0.f, 0.f}, v1[4] = {0.f, 0.f, 0.f, 0.f}, ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < MAX_SPLITK; ++k) {
-    if (k < splitk) {
+  for (int k = 0; k < NL; ++k) {
+    if (SK > 0 || k < splitk) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) v0[c] += q0[k][c];
       if constexpr (DUAL) {
@@ -291,7 +300,14 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a) {
       if constexpr (RMS) ss += qs[k];
     }
   }
-  gemm_epilogue<EPI, DUAL>(a, mb * 64 + lrow, nt, c4, (t & 3) == 0, v0, v1, ss);
+  if constexpr (EPI == EPI_RES) {
+    if (row >= a.M) return;
+    const bf16x4 pk = {f2bf(v0[0] + bf2f(res4[0])), f2bf(v0[1] + bf2f(res4[1])),
+                       f2bf(v0[2] + bf2f(res4[2])), f2bf(v0[3] + bf2f(res4[3]))};
+    *reinterpret_cast<bf16x4*>(a.out + (size_t)row * a.ldo + nt * 16 + c4) = pk;
+    return;
+  }
+  gemm_epilogue<EPI, DUAL>(a, row, nt, c4, (t & 3) == 0, v0, v1, ss);
 }
 
 template <int EPI, bool DUAL>
@@ -312,8 +328,13 @@ static int launch_gemm(const GemmArgs& a, hipStream_t s) {
   }
   if (a.splitk > 1) {
     if (hipError_t e = hipGetLastError()) return (int)e;
-    hipLaunchKernelGGL((splitk_reduce_kernel<EPI, DUAL>), dim3(a.N / 16, (a.M + 63) / 64),
-                       dim3(256), 0, s, a);
+    const dim3 rgrid(a.N / 16, (a.M + 63) / 64);
+    switch (a.splitk) {
+      case 2: hipLaunchKernelGGL((splitk_reduce_kernel<EPI, DUAL, 2>), rgrid, dim3(256), 0, s, a); break;
+      case 4: hipLaunchKernelGGL((splitk_reduce_kernel<EPI, DUAL, 4>), rgrid, dim3(256), 0, s, a); break;
+      case 8: hipLaunchKernelGGL((splitk_reduce_kernel<EPI, DUAL, 8>), rgrid, dim3(256), 0, s, a); break;
+      default: hipLaunchKernelGGL((splitk_reduce_kernel<EPI, DUAL, 0>), rgrid, dim3(256), 0, s, a); break;
+    }
   }
   return (int)hipGetLastError();
 }
