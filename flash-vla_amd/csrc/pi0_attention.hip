@@ -75,19 +75,21 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
   // ---- stage K, V, Q with coalesced loads. The buffer resources end at the last
   // key / query row: rows past the end load as zeros (such keys are masked out
   // below, such query rows are never stored).
+  bf16x8 vv[16];
+  const int row0 = t >> 5, ch = t & 31;                    // 8 rows x 32 chunks per pass
   {
     const int kbytes = max(a.keys - k0, 0) * a.ldkv * (int)sizeof(__bf16);
     const __amdgpu_buffer_rsrc_t kr = rows_rsrc(a.k + (size_t)k0 * a.ldkv, kbytes);
     const __amdgpu_buffer_rsrc_t vr = rows_rsrc(a.v + (size_t)k0 * a.ldkv, kbytes);
     const __amdgpu_buffer_rsrc_t qr =
         rows_rsrc(a.q + (size_t)q0 * a.ldq, max(a.rows - q0, 0) * a.ldq * (int)sizeof(__bf16));
-    const int row0 = t >> 5, ch = t & 31;                  // 8 rows x 32 chunks per pass
     const int koff = (row0 * a.ldkv + ch * 8) * (int)sizeof(__bf16);
     const int kstep = 8 * a.ldkv * (int)sizeof(__bf16);
     const int qoff = (row0 * a.ldq + ch * 8) * (int)sizeof(__bf16);
     const int qstep = 8 * a.ldq * (int)sizeof(__bf16);
-    bf16x8 kv[16], vv[16], qv[2];
-    // issue order = order of use: Q, K, then V (loads return in order)
+    bf16x8 kv[16], qv[2];
+    // issue order = order of use: Q, K, then V (loads return in order). Q and K are
+    // published first; V lands while S = K Q^T and the softmax run.
 #pragma unroll
     for (int j = 0; j < 2; ++j) qv[j] = buf_load8(qr, qoff + j * qstep);
 #pragma unroll
@@ -97,10 +99,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) *reinterpret_cast<bf16x8*>(&qs_[row0 + 8 * j][ch * 8]) = qv[j];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      *reinterpret_cast<bf16x8*>(&ks_[row0 + 8 * j][ch * 8]) = kv[j];
-      *reinterpret_cast<bf16x8*>(&vs_[row0 + 8 * j][ch * 8]) = vv[j];
-    }
+    for (int j = 0; j < 16; ++j) *reinterpret_cast<bf16x8*>(&ks_[row0 + 8 * j][ch * 8]) = kv[j];
   }
   __syncthreads();
   PI0_PROBE(1);
@@ -147,6 +146,10 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
   lsum += __shfl_xor(lsum, 32, PI0_WAVE);
   if (g == 0) { sm[wave][r] = mx; sl[wave][r] = lsum; }
 
+  // ---- publish V (its loads were in flight during S and the softmax)
+#pragma unroll
+  for (int j = 0; j < 16; ++j) *reinterpret_cast<bf16x8*>(&vs_[row0 + 8 * j][ch * 8]) = vv[j];
+  __syncthreads();
   PI0_PROBE(2);
   // ---- O_w = P V_w : B fragment = V[keys kw + {4g..4g+3, 16+4g..16+4g+3}][column]
   f32x4 o[16];
