@@ -852,10 +852,11 @@ int pi0hip_tile_linear(const void* x, int ldx, const void* w_packed, const void*
   TileArgs a = tile_args(x, ldx, w_packed, out, ldo, M, N, K);
   a.bias = (const __bf16*)bias;
   // 64-row tiles unless they overflow one round of the 256 CUs while 96-row tiles fit in
-  // one (vision QKV: 324 -> 216 workgroups); measured at M = 768.
+  // one (vision QKV: 324 -> 216 workgroups at M = 768), or M is large (M >= 2048: the
+  // batched profile, where the taller tiles win by moving fewer bytes per flop).
   const int steps = K / 64;
-  if (N % 128 == 0 && K % 64 == 0 && steps % 3 == 0 && ((M + 63) / 64) * (N / 128) > 256 &&
-      ((M + 95) / 96) * (N / 128) <= 256)
+  if (N % 128 == 0 && K % 64 == 0 && steps % 3 == 0 &&
+      ((((M + 63) / 64) * (N / 128) > 256 && ((M + 95) / 96) * (N / 128) <= 256) || M >= 2048))
     return bias ? launch_tile<96, 32, 3, TE_BIAS, false, 2>(a, s)
                 : launch_tile<96, 32, 3, TE_STORE, false, 2>(a, s);
   return bias ? launch_tile_d4<64, 32, TE_BIAS, false>(a, s)
@@ -869,7 +870,11 @@ int pi0hip_tile_linear_residual(const void* x, int ldx, const void* w_packed, vo
   if (misaligned(x, ldx) || misaligned(out, ldo)) return PI0HIP_ERR_SHAPE;
   TileArgs a = tile_args(x, ldx, w_packed, out, ldo, M, N, K);
   a.splitk = splitk;
-  if (splitk == 1) return launch_tile_d4<64, 32, TE_RES, false>(a, s);
+  if (splitk == 1) {
+    // large M (>= 2048 rows): 128 x 256 tiles fill the chip without splitting K
+    if (M >= 2048 && N % 256 == 0) return launch_tile_d4<128, 64, TE_RES, false>(a, s);
+    return launch_tile_d4<64, 32, TE_RES, false>(a, s);
+  }
   if (N % 4 || ldo % 4) return PI0HIP_ERR_SHAPE;
   if (!ws || ws_bytes < pi0hip_tile_workspace_bytes(M, N, splitk)) return PI0HIP_ERR_WORKSPACE;
   a.part = (float*)ws;
@@ -909,6 +914,7 @@ int pi0hip_tile_qkv_rope_batched(const void* x, int ldx, const void* w_packed, c
   a.out_k = (__bf16*)k; a.out_v = (__bf16*)v; a.ldkv = ldkv;
   a.rope = (const __bf16*)rope; a.heads = heads; a.head_dim = head_dim;
   a.rows_per_batch = rows_per_batch; a.kv_bstride = kv_bstride;
+  if (M >= 2048 && a.N % 256 == 0) return launch_tile_d4<64, 64, TE_QKV_ROPE, false>(a, s);
   return launch_tile_d4<64, 32, TE_QKV_ROPE, false>(a, s);
 }
 
@@ -978,6 +984,7 @@ int pi0hip_tile_linear_bias_res(const void* x, int ldx, const void* w_packed, co
   a.n_valid = N;
   a.bias = (const __bf16*)bias;
   a.res = (const __bf16*)res; a.ldres = ldres; a.res_mod = res_mod;
+  if (M >= 2048) return launch_tile_auto<128, 32, 8, TE_BIAS_RES, false>(a, s);
   return launch_tile_auto<32, 32, 8, TE_BIAS_RES, false>(a, s);
 }
 

@@ -100,9 +100,10 @@ def encoder_norm_gated_ffn(x, gate_w, up_w, out, x_norm):
 
 
 def encoder_ffn_down_residual(x, weight, out):
-    """out += hidden @ weight in place, K = 16384 split four ways (wrappers.py:383-392)."""
-    K = x.shape[1]
-    s = _DOWN_SPLITK if (K // 64) % _DOWN_SPLITK == 0 else 1
+    """out += hidden @ weight in place (wrappers.py:383-392). K = 16384 is split four ways at
+    the single-request size; from 2048 rows up the row tiles alone fill the chip."""
+    M, K = x.shape
+    s = _DOWN_SPLITK if (K // 64) % _DOWN_SPLITK == 0 and M < 2048 else 1
     return _tile_residual(x, weight, out, s, "enc_ffn_down")
 
 

@@ -93,7 +93,7 @@ def test_projector():
                                pb.float()), what="projector")
 
 
-@pytest.mark.parametrize("M", [768, 816, 40])
+@pytest.mark.parametrize("M", [768, 816, 40, 3264])
 def test_norm_qkv_rope(M):
     x = rnd((M, 2048), 17, 1.0)
     w = rnd((2048, 2560), 18, 0.02)
@@ -118,7 +118,7 @@ def test_encoder_attention(rows, keys):
     close(out.reshape(rows, 256), ref, tol=2.0 ** -5, what=f"attention {rows}x{keys}")
 
 
-@pytest.mark.parametrize("M", [768, 100])
+@pytest.mark.parametrize("M", [768, 100, 3264])
 def test_out_proj_residual(M):
     x, w, r = rnd((M, 2048), 22), rnd((2048, 2048), 23, 0.02), rnd((M, 2048), 24)
     out = r.to(DEV).clone()
@@ -137,6 +137,17 @@ def test_ffn_down_splitk_deterministic():
     EW.encoder_ffn_down_residual(xd, wd, out2)
     assert torch.equal(out1, out2)
     close(out1, E.enc_residual(x.float(), w.float(), r.float()), what="ffn_down")
+
+
+def test_ffn_down_large_m():
+    """Batched prefix (4 x 816 rows): the row tiles fill the chip, K is not split; the fp32
+    oracle arithmetic runs on the device to keep the 219-GFLOP reference fast."""
+    M = 3264
+    x, w, r = rnd((M, 16384), 31, 0.5), rnd((16384, 2048), 32, 0.02), rnd((M, 2048), 33)
+    out = r.to(DEV).clone()
+    EW.encoder_ffn_down_residual(x.to(DEV), w.to(DEV), out)
+    ref = E.enc_residual(x.to(DEV).float(), w.to(DEV).float(), r.to(DEV).float())
+    close(out, ref, what="ffn_down M=3264")
 
 
 @pytest.mark.parametrize("M", [768, 816])

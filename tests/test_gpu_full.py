@@ -110,6 +110,32 @@ def test_ffn_up_gelu_ragged_n():
     assert torch.all(store[768 * 4304:] == 7.0), "stored past the 4304 valid columns"
 
 
+@pytest.mark.parametrize("views", [12])
+def test_large_m_vision_gemms(views):
+    """Batched profile (4 requests x 3 views = 3072 rows): QKV, o-proj and FFN-down run on the
+    taller large-M tiles; references in fp32 on the device."""
+    M = views * 256
+    x = rnd((views, 256, 1152), 83)
+    nw, nb = rnd(1152, 84, 0.5), rnd(1152, 85, 0.5)
+    wq, bq = rnd((1152, 3456), 86, 0.03), rnd(3456, 87, 0.5)
+    qkv = torch.zeros(views, 256, 3456, dtype=torch.bfloat16, device=DEV)
+    xn = torch.zeros(views, 256, 1152, dtype=torch.bfloat16, device=DEV)
+    VW.vision_norm_qkv(x.to(DEV), nw.to(DEV), nb.to(DEV), wq.to(DEV), bq.to(DEV), qkv, xn)
+    ref_n = E.enc_layer_norm(x.to(DEV).float().reshape(M, 1152), nw.to(DEV).float(), nb.to(DEV).float())
+    close(qkv.reshape(M, 3456), (ref_n @ wq.to(DEV).float() + bq.to(DEV).float()).bfloat16().float(),
+          what=f"vision qkv M={M}")
+    a, wo, bo, r = rnd((views, 256, 1152), 88), rnd((1152, 1152), 89, 0.03), rnd(1152, 90), rnd((views, 256, 1152), 91)
+    out = r.to(DEV).clone()
+    VW.vision_out_proj_residual(a.to(DEV), wo.to(DEV), bo.to(DEV), out, out)
+    ref = a.to(DEV).float().reshape(M, 1152) @ wo.to(DEV).float() + bo.to(DEV).float() + r.to(DEV).float().reshape(M, 1152)
+    close(out.reshape(M, 1152), ref.bfloat16().float(), what=f"vision o_proj M={M}")
+    h, wd, bd = rnd((views, 256, 4304), 92, 0.5), rnd((4304, 1152), 93, 0.02), rnd(1152, 94)
+    out = r.to(DEV).clone()
+    VW.vision_ffn_down_residual(h.to(DEV), wd.to(DEV), bd.to(DEV), out, out)
+    ref = h.to(DEV).float().reshape(M, 4304) @ wd.to(DEV).float() + bd.to(DEV).float() + r.to(DEV).float().reshape(M, 1152)
+    close(out.reshape(M, 1152), ref.bfloat16().float(), what=f"vision ffn_down M={M}")
+
+
 def test_ffn_down_ragged_k():
     """K = 4304: the packed weight's zero rows 4304..4351 meet the next row's values."""
     h, w, b, r = rnd((3, 256, 4304), 79, 0.5), rnd((4304, 1152), 80, 0.02), rnd(1152, 81), rnd((3, 256, 1152), 82)
