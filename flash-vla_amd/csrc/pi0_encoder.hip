@@ -365,12 +365,18 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const __bf16* __restric
   if (row >= M) return;
   const int chunks = K >> 3;
   const __bf16* xr = x + (size_t)row * ldx;
-  bf16x8 v[4];
-  float s = 0.f, ss = 0.f;
+  bf16x8 v[4], wv[4], bv[4];
+  // the row and the affine parameters are requested together: one memory round trip
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
     const int ch = c * 64 + lane;
     v[c] = ch < chunks ? load8(xr + ch * 8) : zero8();
+    wv[c] = ch < chunks ? load8(w + ch * 8) : zero8();
+    bv[c] = ch < chunks ? load8(b + ch * 8) : zero8();
+  }
+  float s = 0.f, ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) { const float f = bf2f(v[c][j]); s += f; ss += f * f; }
   }
@@ -383,10 +389,10 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const __bf16* __restric
   for (int c = 0; c < 4; ++c) {
     const int ch = c * 64 + lane;
     if (ch >= chunks) continue;
-    const bf16x8 wv = load8(w + ch * 8), bv = load8(b + ch * 8);
     bf16x8 o;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = f2bf((bf2f(v[c][j]) - mean) * inv * bf2f(wv[j]) + bf2f(bv[j]));
+    for (int j = 0; j < 8; ++j)
+      o[j] = f2bf((bf2f(v[c][j]) - mean) * inv * bf2f(wv[c][j]) + bf2f(bv[c][j]));
     *reinterpret_cast<bf16x8*>(orow + ch * 8) = o;
   }
 }
