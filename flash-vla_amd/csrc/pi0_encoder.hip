@@ -654,7 +654,7 @@ struct VisAttnArgs {
   float scale_log2;
 };
 
-__global__ __launch_bounds__(64) void vision_attn_kernel(VisAttnArgs a) {
+__global__ __launch_bounds__(64, 1) void vision_attn_kernel(VisAttnArgs a) {
   const int lane = threadIdx.x, r = lane & 31, h = lane >> 5;
   const int qt = blockIdx.x, head = blockIdx.y, view = blockIdx.z;
   const size_t row0 = (size_t)view * VA_TOK;
@@ -673,25 +673,33 @@ __global__ __launch_bounds__(64) void vision_attn_kernel(VisAttnArgs a) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
   const __bf16* vt = a.vt + (((size_t)view * a.heads + head) * VA_HDP) * VA_TOK;
-  for (int kb = 0; kb < VA_TOK / 32; ++kb) {
-    bf16x8 kf[5];
+  // A three-slot register ring over the 8 key blocks: block kb + 3 is requested as soon
+  // as block kb has consumed its slot, so two blocks are always in flight.
+  constexpr int NB = VA_TOK / 32, RS = 3;
+  bf16x8 kf[RS][5], vf[RS][3][2];
+  auto load_blk = [&](int kb) {
+    const int sl = kb % RS;
+    // columns 72..79 of the padded head are read unmasked (the next head's K, or for the
+    // last head the first V columns of the same row): Q^T is zero there, so they add 0
 #pragma unroll
-    for (int kk = 0; kk < 5; ++kk) {
-      const int d = kk * 16 + h * 8;
-      kf[kk] = d < VA_HD ? load8(a.qkv + (row0 + kb * 32 + r) * a.ldqkv + a.dim + head * VA_HD + d)
-                         : zero8();
-    }
-    bf16x8 vf[3][2];
+    for (int kk = 0; kk < 5; ++kk)
+      kf[sl][kk] = load8(a.qkv + (row0 + kb * 32 + r) * a.ldqkv + a.dim + head * VA_HD + kk * 16 + h * 8);
 #pragma unroll
     for (int dt = 0; dt < 3; ++dt)
 #pragma unroll
       for (int c = 0; c < 2; ++c)
-        vf[dt][c] = load8(vt + (size_t)(dt * 32 + r) * VA_TOK + kb * 32 + 16 * c + 8 * h);
+        vf[sl][dt][c] = load8(vt + (size_t)(dt * 32 + r) * VA_TOK + kb * 32 + 16 * c + 8 * h);
+  };
+#pragma unroll
+  for (int kb = 0; kb < RS; ++kb) load_blk(kb);
+#pragma unroll
+  for (int kb = 0; kb < NB; ++kb) {
+    const int sl = kb % RS;
     f32x16 st;
 #pragma unroll
     for (int e = 0; e < 16; ++e) st[e] = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < 5; ++kk) st = mfma32(kf[kk], qf[kk], st);
+    for (int kk = 0; kk < 5; ++kk) st = mfma32(kf[sl][kk], qf[kk], st);
     float mx = -1.0e30f;
 #pragma unroll
     for (int e = 0; e < 16; ++e) { st[e] *= a.scale_log2; mx = fmaxf(mx, st[e]); }
@@ -713,9 +721,11 @@ __global__ __launch_bounds__(64) void vision_attn_kernel(VisAttnArgs a) {
     for (int dt = 0; dt < 3; ++dt) {
       f32x16 acc = o[dt] * alpha;
 #pragma unroll
-      for (int c = 0; c < 2; ++c) acc = mfma32(vf[dt][c], pf[c], acc);
+      for (int c = 0; c < 2; ++c) acc = mfma32(vf[sl][dt][c], pf[c], acc);
       o[dt] = acc;
     }
+    if (kb + RS < NB) load_blk(kb + RS);
+    __builtin_amdgcn_sched_barrier(0);                 // keep each refill in its iteration
   }
   // lane holds O^T[d = 32 dt + 8 (e / 4) + 4 h + e % 4][query r]
   const float inv = __builtin_amdgcn_rcpf(l_run);
