@@ -430,20 +430,32 @@ struct EncAttnArgs {
 __global__ __launch_bounds__(256) void transpose_v_kernel(const __bf16* __restrict__ v, int ldv,
                                                           __bf16* __restrict__ vt, int ldvt,
                                                           int keys, long long v_bstride) {
-  __shared__ __bf16 tile[64][66];
+  __shared__ __attribute__((aligned(16))) __bf16 tile[64][72];
   const int k0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
   v += (size_t)blockIdx.z * v_bstride;
   vt += (size_t)blockIdx.z * EA_HD * ldvt;
   const int t = threadIdx.x;
-  for (int i = t; i < 64 * 64; i += 256) {
-    const int kr = i >> 6, dc = i & 63;
-    tile[kr][dc] = (k0 + kr < keys) ? v[(size_t)(k0 + kr) * ldv + d0 + dc] : __bf16(0.f);
+  // 16-byte loads: key row kr, dims 8 c .. + 7 (keys past the end read as zeros)
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int i = t + 256 * j, kr = i >> 3, c = (i & 7) * 8;
+    const bf16x8 x = k0 + kr < keys ? load8(v + (size_t)(k0 + kr) * ldv + d0 + c) : zero8();
+    *reinterpret_cast<bf16x8*>(&tile[kr][c]) = x;
   }
   __syncthreads();
-  for (int i = t; i < 64 * 64; i += 256) {
-    const int dr = i >> 6, kc = i & 63;      // kc = storage slot; its key:
-    const int sl = kc & 15, key = (kc & ~15) + ((sl & 4) ? 8 : 0) + ((sl & 8) ? 4 : 0) + (sl & 3);
-    vt[(size_t)(d0 + dr) * ldvt + k0 + kc] = tile[key][dr];
+  // 16-byte stores: V^T row d0 + dr, storage slots 8 c .. + 7 (each slot's key permuted
+  // into the P^T order of the attention's S^T accumulator)
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int i = t + 256 * j, dr = i >> 3, c = (i & 7) * 8;
+    bf16x8 o;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int kc = c + q, sl = kc & 15;
+      const int key = (kc & ~15) + ((sl & 4) ? 8 : 0) + ((sl & 8) ? 4 : 0) + (sl & 3);
+      o[q] = tile[key][dr];
+    }
+    *reinterpret_cast<bf16x8*>(vt + (size_t)(d0 + dr) * ldvt + k0 + c) = o;
   }
 }
 
@@ -629,20 +641,28 @@ constexpr int VA_TOK = 256, VA_HD = 72, VA_HDP = 96;
 __global__ __launch_bounds__(256) void vision_vt_kernel(const __bf16* __restrict__ qkv, int ldqkv,
                                                         __bf16* __restrict__ vt, int heads,
                                                         int dim) {
-  __shared__ __bf16 tile[64][VA_HD + 1];
+  __shared__ __attribute__((aligned(16))) __bf16 tile[64][VA_HD + 8];
   const int kc = blockIdx.x, head = blockIdx.y, view = blockIdx.z;
   const int t = threadIdx.x;
   const __bf16* src = qkv + ((size_t)view * VA_TOK + kc * 64) * ldqkv + 2 * dim + head * VA_HD;
-  for (int i = t; i < 64 * VA_HD; i += 256) {
-    const int kr = i / VA_HD, d = i - kr * VA_HD;
-    tile[kr][d] = src[(size_t)kr * ldqkv + d];
+  // 16-byte loads: 64 key rows x 9 chunks of 8 head dims
+  for (int i = t; i < 64 * 9; i += 256) {
+    const int kr = i / 9, c = (i - kr * 9) * 8;
+    *reinterpret_cast<bf16x8*>(&tile[kr][c]) = load8(src + (size_t)kr * ldqkv + c);
   }
   __syncthreads();
+  // 16-byte stores: 96 padded dims x 8 chunks of 8 storage slots (keys in P^T slot order)
   __bf16* dst = vt + (((size_t)view * heads + head) * VA_HDP) * VA_TOK + kc * 64;
-  for (int i = t; i < 64 * VA_HDP; i += 256) {
-    const int d = i >> 6, slot = i & 63;
-    const int sl = slot & 15, key = (slot & ~15) + ((sl & 4) ? 8 : 0) + ((sl & 8) ? 4 : 0) + (sl & 3);
-    dst[(size_t)d * VA_TOK + slot] = d < VA_HD ? tile[key][d] : __bf16(0.f);
+  for (int i = t; i < VA_HDP * 8; i += 256) {
+    const int d = i >> 3, c = (i & 7) * 8;
+    bf16x8 o;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int slot = c + q, sl = slot & 15;
+      const int key = (slot & ~15) + ((sl & 4) ? 8 : 0) + ((sl & 8) ? 4 : 0) + (sl & 3);
+      o[q] = d < VA_HD ? tile[key][d] : __bf16(0.f);
+    }
+    *reinterpret_cast<bf16x8*>(dst + (size_t)d * VA_TOK + c) = o;
   }
 }
 
@@ -967,7 +987,8 @@ int pi0hip_encoder_attention_batched(const void* q, int ldq, const void* k, cons
                                      int keys, int head_dim, float scale, int batch, void* ws,
                                      size_t ws_bytes, hipStream_t s) {
   if (!q || !k || !v || !out || rows <= 0 || keys <= 0 || batch <= 0) return PI0HIP_ERR_ARG;
-  if (head_dim != EA_HD || misaligned(q, ldq) || misaligned(k, ldkv) || (ldo & 3) ||
+  if (head_dim != EA_HD || misaligned(q, ldq) || misaligned(k, ldkv) || misaligned(v, ldkv) ||
+      (ldo & 3) ||
       (reinterpret_cast<uintptr_t>(out) & 7) || (kv_bstride & 7))
     return PI0HIP_ERR_SHAPE;
   if (!ws || ws_bytes < pi0hip_encoder_attention_batched_workspace_bytes(keys, batch))
