@@ -83,7 +83,13 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
 // re-load the last step into the free slot), so "A of step s has landed" is the
 // fixed count vmcnt <= LB + (D - 2) * (LA + LB) of loads issued after it; a plain
 // s_barrier (no fence: the fence would wait for every prefetch) then publishes it.
-template <int BM, int WN, int D, int EPI, bool DUAL, int OCC>
+//
+// RMS = 1 fuses the decoder's RMS pre-norm for its batched gated FFN (fused_norm.py:26-78):
+// the block sees every k of its rows, so each row's sum of squares is accumulated from
+// the A fragments it already reads (v_dot2 on bf16 pairs; row tile i by wave i % 4),
+// f = bf16(rsqrt(mean(x^2) + 1e-6)) goes to LDS and the epilogue forms
+// gelu(f * x@Wg) * (f * x@Wu) from the fp32 accumulators.
+template <int BM, int WN, int D, int EPI, bool DUAL, int OCC, int RMS = 0>
 __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
   constexpr int BN = 4 * WN;               // B columns per workgroup
   constexpr int FM = BM / 32;              // 32-row fragments (every wave holds all rows)
@@ -100,8 +106,12 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
   constexpr int RING = D * TA * 64;                  // 16-byte slots of the operand ring
   constexpr int PARK = (BM * CP * 4 + 15) / 16;
   __shared__ bf16x8 lds[RING > PARK ? RING : PARK];
+  __shared__ float rms_f[RMS ? BM : 1];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  float ssr[FM];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) ssr[i] = 0.f;
   int id = blockIdx.x;
   if (a.xcd_remap) id = (id & 7) * (gridDim.x >> 3) + (id >> 3);
   const int mt = id % a.tiles_m;
@@ -181,11 +191,30 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
         __builtin_amdgcn_sched_barrier(0);   // keep the prefetch ahead of these MFMAs
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(ap[f % PF], breg[u][j][kq], acc[i][j]);
+        if constexpr (RMS) {
+          if (wave == (i & 3)) {
+            typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+            const bf16x8 v = ap[f % PF];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+              const bf16x2_t q = {v[2 * p], v[2 * p + 1]};
+              ssr[i] = __builtin_amdgcn_fdot2_f32_bf16(q, q, ssr[i], false);
+            }
+          }
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
   __builtin_amdgcn_s_waitcnt(PI0_VMCNT(0));   // drain the dummy tail loads before exit
+  if constexpr (RMS) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      if (wave != (i & 3)) continue;
+      const float ss = ssr[i] + __shfl_xor(ssr[i], 32);    // the two k halves of row lane % 32
+      if (lane < 32) rms_f[i * 32 + lane] = round_bf(rsqrtf(ss / (float)a.K + 1e-6f));
+    }
+  }
 
   // ---- epilogue through LDS (the ring is free now): the waves park their fp32 tiles
   // row-major, then every thread finishes 8 consecutive output columns of a row with
@@ -201,10 +230,11 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
       for (int e = 0; e < 16; ++e) {
         const int row = i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
         if constexpr (DUAL) {
+          const float fr = RMS ? rms_f[row] : 1.f;
 #pragma unroll
           for (int j = 0; j < FN / 2; ++j)
             cs[row * CP + (wave * (FN / 2) + j) * 32 + r] =
-                gelu_tanh(acc[i][j][e]) * acc[i][FN / 2 + j][e];
+                gelu_tanh(fr * acc[i][j][e]) * (fr * acc[i][FN / 2 + j][e]);
         } else {
 #pragma unroll
           for (int j = 0; j < FN; ++j) cs[row * CP + (wave * FN + j) * 32 + r] = acc[i][j][e];
@@ -791,7 +821,7 @@ using namespace pi0;
 
 // ---- host-side launch helpers ----------------------------------------------------
 
-template <int BM, int WN, int D, int EPI, bool DUAL, int OCC>
+template <int BM, int WN, int D, int EPI, bool DUAL, int OCC, int RMS = 0>
 static int launch_tile(TileArgs a, hipStream_t s) {
   a.tiles_m = (a.M + BM - 1) / BM;
   const int bn_out = DUAL ? 2 * WN : 4 * WN;
@@ -803,19 +833,19 @@ static int launch_tile(TileArgs a, hipStream_t s) {
   const int grid = a.tiles_m * a.tiles_n * a.splitk;
   // XCD-contiguous tile order needs a grid divisible by the 8 XCDs
   a.xcd_remap = (grid % 8 == 0) ? 1 : 0;
-  hipLaunchKernelGGL((tile_gemm_kernel<BM, WN, D, EPI, DUAL, OCC>), dim3(grid), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((tile_gemm_kernel<BM, WN, D, EPI, DUAL, OCC, RMS>), dim3(grid), dim3(256), 0, s, a);
   return (int)hipGetLastError();
 }
 
 // Pipeline depth: the deepest even ring (<= DMAX) whose depth divides the per-split step count.
-template <int BM, int WN, int DMAX, int EPI, bool DUAL, int OCC = 1>
+template <int BM, int WN, int DMAX, int EPI, bool DUAL, int OCC = 1, int RMS = 0>
 static int launch_tile_auto(TileArgs a, hipStream_t s) {
   if (a.K % 64 || a.splitk < 1 || (a.K / 64) % a.splitk) return PI0HIP_ERR_SHAPE;
   const int steps = a.K / 64 / a.splitk;
-  if (DMAX >= 8 && steps % 8 == 0) return launch_tile<BM, WN, (DMAX >= 8 ? 8 : 2), EPI, DUAL, OCC>(a, s);
-  if (DMAX >= 6 && steps % 6 == 0) return launch_tile<BM, WN, (DMAX >= 6 ? 6 : 2), EPI, DUAL, OCC>(a, s);
-  if (DMAX >= 4 && steps % 4 == 0) return launch_tile<BM, WN, (DMAX >= 4 ? 4 : 2), EPI, DUAL, OCC>(a, s);
-  if (steps % 2 == 0) return launch_tile<BM, WN, 2, EPI, DUAL, OCC>(a, s);
+  if (DMAX >= 8 && steps % 8 == 0) return launch_tile<BM, WN, (DMAX >= 8 ? 8 : 2), EPI, DUAL, OCC, RMS>(a, s);
+  if (DMAX >= 6 && steps % 6 == 0) return launch_tile<BM, WN, (DMAX >= 6 ? 6 : 2), EPI, DUAL, OCC, RMS>(a, s);
+  if (DMAX >= 4 && steps % 4 == 0) return launch_tile<BM, WN, (DMAX >= 4 ? 4 : 2), EPI, DUAL, OCC, RMS>(a, s);
+  if (steps % 2 == 0) return launch_tile<BM, WN, 2, EPI, DUAL, OCC, RMS>(a, s);
   return PI0HIP_ERR_SHAPE;
 }
 
@@ -914,7 +944,10 @@ int pi0hip_tile_linear_residual(const void* x, int ldx, const void* w_packed, vo
   if (N % 4 || ldo % 4) return PI0HIP_ERR_SHAPE;
   if (!ws || ws_bytes < pi0hip_tile_workspace_bytes(M, N, splitk)) return PI0HIP_ERR_WORKSPACE;
   a.part = (float*)ws;
-  if (int e = launch_tile_auto<192, 32, 4, TE_PARTIAL, false>(a, s)) return e;
+  // small M (the batched decoder, 204 rows): 32-row tiles, two workgroups per CU
+  if (int e = M <= 256 ? launch_tile_auto<32, 32, 4, TE_PARTIAL, false, 2>(a, s)
+                       : launch_tile_auto<192, 32, 4, TE_PARTIAL, false>(a, s))
+    return e;
   hipLaunchKernelGGL(tile_reduce_res_kernel, dim3((M * (N / 4) + 255) / 256), dim3(256), 0, s, a);
   return (int)hipGetLastError();
 }
@@ -926,6 +959,16 @@ int pi0hip_tile_gated_ffn(const void* x, int ldx, const void* gate_packed, const
   TileArgs a = tile_args(x, ldx, gate_packed, out, ldo, M, N, K);
   a.w1 = (const __bf16*)up_packed;
   return launch_tile_auto<128, 64, 2, TE_GATE, true, 2>(a, s);
+}
+
+int pi0hip_tile_norm_gated_ffn(const void* x, int ldx, const void* gate_packed,
+                               const void* up_packed, void* out, int ldo, int M, int N, int K,
+                               hipStream_t s) {
+  if (!x || !gate_packed || !up_packed || !out || bad_dims(M, N, K)) return PI0HIP_ERR_ARG;
+  if (misaligned(x, ldx) || misaligned(out, ldo) || K % 128) return PI0HIP_ERR_SHAPE;
+  TileArgs a = tile_args(x, ldx, gate_packed, out, ldo, M, N, K);
+  a.w1 = (const __bf16*)up_packed;
+  return launch_tile_auto<32, 64, 2, TE_GATE, true, 1, 1>(a, s);
 }
 
 int pi0hip_tile_qkv_rope(const void* x, int ldx, const void* w_packed, const void* rope, void* q,

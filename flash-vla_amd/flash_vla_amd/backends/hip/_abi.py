@@ -59,6 +59,7 @@ PROTOTYPES = {
     "pi0hip_tile_linear_residual": (c_int, [P, c_int, P, P, c_int, c_int, c_int, c_int, c_int,
                                             P, c_size_t, P]),
     "pi0hip_tile_gated_ffn": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, P]),
+    "pi0hip_tile_norm_gated_ffn": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int, P]),
     "pi0hip_tile_qkv_rope": (c_int, [P, c_int, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int,
                                      P]),
     "pi0hip_encoder_attention_workspace_bytes": (c_size_t, [c_int]),

@@ -283,12 +283,24 @@ def decoder_attention(Q, K, V, scores, out, encoder_seq_len):
     return out
 
 
+# Above one 64-row block (the batched decoder, M = B x 51) the decoder's GEMMs run on the
+# prefix encoder's tile kernel: the skinny kernel would stream the weights once per row block.
+_TILE_M = 64
+
+
 def _residual(x, weight, out, role):
     _check(x, "x", 2); _check(out, "out", 2)
     M, K = x.shape
     N = weight.shape[1]
     if weight.shape[0] != K or out.shape != (M, N):
         raise ValueError(f"{role}: shape mismatch")
+    if M > _TILE_M and K % 256 == 0 and N % 128 == 0:
+        s = 4
+        nbytes = _abi.lib().pi0hip_tile_workspace_bytes(M, N, s)
+        ws = scratch(f"tile_ws_{role}", (nbytes,), torch.uint8, x.device)
+        _abi.call("pi0hip_tile_linear_residual", _ptr(x), x.stride(0), packed_weight_ptr(weight, 32),
+                  _ptr(out), out.stride(0), M, N, K, s, ws.data_ptr(), nbytes, _stream())
+        return out
     wp = packed_weight_ptr(weight)
     s = _splitk(M, N, K)
     ws, nbytes = _gemm_ws(f"gemm_ws_{role}", M, N, s, 0, x.device)
@@ -313,6 +325,10 @@ def _gated_ffn(x, gate_w, up_w, out):
     N = gate_w.shape[1]
     if gate_w.shape != (K, N) or up_w.shape != (K, N) or out.shape != (M, N):
         raise ValueError("decoder_norm_gated_ffn: shape mismatch")
+    if M > _TILE_M and K % 128 == 0 and N % 128 == 0:
+        _abi.call("pi0hip_tile_norm_gated_ffn", _ptr(x), x.stride(0), packed_weight_ptr(gate_w, 32),
+                  packed_weight_ptr(up_w, 32), _ptr(out), out.stride(0), M, N, K, _stream())
+        return out
     gp = packed_weight_ptr(gate_w)
     up = packed_weight_ptr(up_w)
     _abi.call("pi0hip_norm_gated_ffn", _ptr(x), x.stride(0), gp, up, _ptr(out), out.stride(0),

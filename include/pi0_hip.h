@@ -173,6 +173,15 @@ int pi0hip_tile_linear_residual(const void* x, int ldx, const void* w_packed, vo
 int pi0hip_tile_gated_ffn(const void* x, int ldx, const void* gate_packed, const void* up_packed,
                           void* out, int ldo, int M, int N, int K, hipStream_t s);
 
+/* out = bf16(gelu_tanh(f * x @ Wg) * (f * x @ Wu)) with the decoder's fused RMS pre-norm
+ * f = bf16(rsqrt(mean_k x^2 + 1e-6)) per row of the raw input x; packed weights in the
+ * 16 k x 32 n (pi0hip_pack_weight32) order; K % 128 == 0, N % 128 == 0. The batched
+ * decoder's gated FFN (M > 64 rows): decoder_norm_gated_ffn, fused_wrappers.py:45-54
+ * (tl_fused_rms_gate, kernels/fused_norm.py:26-78). */
+int pi0hip_tile_norm_gated_ffn(const void* x, int ldx, const void* gate_packed,
+                               const void* up_packed, void* out, int ldo, int M, int N, int K,
+                               hipStream_t s);
+
 /* proj = bf16(x @ W), W = [K, (heads + 2) * head_dim]; RoPE (interleaved pairs,
  * table rope[M, head_dim]) on the rounded Q and K columns, then scatter to
  * q [M, heads*head_dim], k / v rows [M, ldkv].

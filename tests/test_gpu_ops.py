@@ -137,18 +137,20 @@ def test_attention_state_rows_ignore_action_keys():
     assert not torch.equal(outs[0][8:], outs[1][8:])
 
 
-@pytest.mark.parametrize("K", [2048, 4096])
-def test_residual_gemm(K):
-    x = rnd((51, K), 21)
+@pytest.mark.parametrize("M,K", [(51, 2048), (51, 4096), (204, 2048), (204, 4096), (100, 4096)])
+def test_residual_gemm(M, K):
+    """M > 64 (the batched decoder) runs on the tile kernel's split-K path."""
+    x = rnd((M, K), 21)
     w = rnd((K, 1024), 22, 0.02)
-    r = rnd((51, 1024), 23)
+    r = rnd((M, 1024), 23)
     out = r.to(DEV)
     W.decoder_out_proj_residual(x.to(DEV), w.to(DEV), out)
-    close(out, O.op_matmul_residual(x.float(), w.float(), r.float()), what=f"res K={K}")
+    close(out, O.op_matmul_residual(x.float(), w.float(), r.float()), what=f"res M={M} K={K}")
 
 
-def test_residual_splitk_is_deterministic_and_reentrant():
-    x, w, r = rnd((51, 4096), 24).to(DEV), rnd((4096, 1024), 25, 0.02).to(DEV), rnd((51, 1024), 26)
+@pytest.mark.parametrize("M", [51, 204])
+def test_residual_splitk_is_deterministic_and_reentrant(M):
+    x, w, r = rnd((M, 4096), 24).to(DEV), rnd((4096, 1024), 25, 0.02).to(DEV), rnd((M, 1024), 26)
     outs = []
     for _ in range(3):
         out = r.to(DEV)
@@ -157,13 +159,14 @@ def test_residual_splitk_is_deterministic_and_reentrant():
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
 
 
-@pytest.mark.parametrize("M", [51, 7])
+@pytest.mark.parametrize("M", [51, 7, 204, 100])
 def test_norm_gated_ffn(M):
+    """M > 64 runs on the tile kernel with the RMS factor fused (f rounded to bf16)."""
     x = rnd((M, 1024), 27)
     wg, wu = rnd((1024, 4096), 28, 0.02), rnd((1024, 4096), 29, 0.02)
     out = torch.zeros(M, 4096, dtype=torch.bfloat16, device=DEV)
     W.decoder_norm_gated_ffn(x.to(DEV), wg.to(DEV), wu.to(DEV), out, None)
-    close(out, O.op_norm_gated_ffn(x.float(), wg.float(), wu.float()), what="gated_ffn")
+    close(out, O.op_norm_gated_ffn(x.float(), wg.float(), wu.float()), what=f"gated_ffn M={M}")
 
 
 def test_action_out_proj_euler_update():
