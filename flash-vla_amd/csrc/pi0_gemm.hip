@@ -182,6 +182,7 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int it = 0; it < XIT; ++it) *reinterpret_cast<bf16x8*>(xl + it * RPI * XP) = xv[it];
   }
+  PI0_PROBE(3);
   // (each wave reads only the rows it staged itself: no workgroup barrier needed)
 
   const int r = lane & 15, g = lane >> 4;
@@ -196,12 +197,16 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
       const bf16x8 av = *reinterpret_cast<const bf16x8*>(xs + (mt * 16 + r) * XP + i * 32 + g * 8);
       acc0[mt] = mfma16(av, b0[i], acc0[mt]);
       if constexpr (DUAL) acc1[mt] = mfma16(av, b1[i], acc1[mt]);
-      if constexpr (RMS) {
+      if constexpr (RMS) {       // sum of squares with v_dot2 (two bf16 products per op)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) { const float v = bf2f(av[j]); ssl[mt] += v * v; }
+        for (int j = 0; j < 4; ++j) {
+          const bf16x2 q = {av[2 * j], av[2 * j + 1]};
+          ssl[mt] = __builtin_amdgcn_fdot2_f32_bf16(q, q, ssl[mt], false);
+        }
       }
     }
   }
+  PI0_PROBE(4);
   __syncthreads();                        // x staging area becomes the reduction area
 
   // ---- intra-workgroup reduction over the 4 waves' K ranges
@@ -220,6 +225,7 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   }
   __syncthreads();
 
+  PI0_PROBE(5);
   // thread t owns row t/4 (of 64) and columns 4*(t%4) .. +3 of the tile
   const int lrow = t >> 2, c4 = (t & 3) * 4;
   const int mt = lrow >> 4, r16 = lrow & 15, ii = r16 & 3, gg = r16 >> 2;
@@ -255,6 +261,7 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
     return;
   }
   gemm_epilogue<EPI, DUAL>(a, m0 + lrow, nt, c4, (t & 3) == 0, v0, v1, ss);
+  PI0_PROBE(6);
 }
 
 
