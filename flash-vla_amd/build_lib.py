@@ -43,14 +43,48 @@ def _compile(src: str) -> str:
 _PACKED_FP32 = re.compile(r"\bv_pk_(add|mul|fma)_f32\b")
 
 
-def check_no_packed_fp32(src: str) -> None:
-    """Compile `src` to device assembly and fail if any packed fp32 VALU op was generated."""
+def check_kblock_waits(asm: str) -> list[str]:
+    """Names of skinny GEMM kernels whose k-block waits do not cover their LDS copies.
+
+    skinny_gemm_kernel issues, per k-block, buffer loads that write x straight into
+    LDS and then that k-block's weight loads; before the MFMAs of k-block j it waits
+    with vmcnt(N). Vector-memory operations complete in issue order, so the wait is
+    sufficient only if N is at most the number of operations issued after k-block j's
+    last LDS copy. This re-checks that order in the generated code (the scheduling
+    barriers in the source are what keep it).
+    """
+    bad = []
+    for m in re.finditer(r"^(_ZN3pi018skinny_gemm_kernelI\w+):", asm, re.M):
+        body = asm[m.end():asm.index("s_endpgm", m.end())]
+        lines = [ln.strip() for ln in body.split("\n")]
+        first_ds = next(i for i, ln in enumerate(lines) if ln.startswith("ds_read"))
+        issue = [i for i, ln in enumerate(lines[:first_ds])
+                 if ln.startswith(("global_load", "buffer_load"))]
+        kinds = ["lds" if lines[i].endswith(" lds") else "reg" for i in issue]
+        last_copy = [j for j, k in enumerate(kinds)
+                     if k == "lds" and (j + 1 == len(kinds) or kinds[j + 1] != "lds")]
+        waits = [int(w) for w in re.findall(r"s_waitcnt vmcnt\((\d+)\)",
+                                            "\n".join(lines[issue[-1] + 1:]))]
+        ok = bool(last_copy) and len(waits) >= len(last_copy) and all(
+            waits[j] <= len(kinds) - 1 - c for j, c in enumerate(last_copy))
+        if not ok:
+            bad.append(m.group(1))
+    return bad
+
+
+def check_device_code(src: str) -> None:
+    """Compile `src` to device assembly and fail if any packed fp32 VALU op was
+    generated, or (pi0_gemm.hip) if a skinny GEMM's k-block waits are unsafe."""
     cmd = [HIPCC, *FLAGS, "--cuda-device-only", "-S", src, "-o", "-"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc -S failed for {src}:\n{res.stderr}")
     if _PACKED_FP32.search(res.stdout):
         raise RuntimeError(f"{src}: packed fp32 VALU instructions in the device code")
+    if os.path.basename(src) == "pi0_gemm.hip":
+        bad = check_kblock_waits(res.stdout)
+        if bad:
+            raise RuntimeError(f"{src}: k-block vmcnt waits do not cover the LDS copies in {bad}")
 
 
 def build(verbose: bool = False, check_isa: bool = True) -> str:
@@ -60,7 +94,7 @@ def build(verbose: bool = False, check_isa: bool = True) -> str:
     with cf.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
         objs = list(ex.map(_compile, sources))
         if check_isa:
-            list(ex.map(check_no_packed_fp32, sources))
+            list(ex.map(check_device_code, sources))
     tmp = LIB + ".tmp"
     # --no-undefined: a kernel whose host stub was not emitted fails here, not at load time
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", *objs,

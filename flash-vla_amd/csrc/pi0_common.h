@@ -27,6 +27,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 #define PI0_PROBE(i) ((void)0)
 #endif
 
+// s_waitcnt immediate: vmcnt(n) with the other counters left alone (gfx9 encoding:
+// vmcnt bits 3:0 and 15:14).
+#define PI0_VMCNT(n) (((n) & 0xF) | (0x7 << 4) | (0xF << 8) | (((n) >> 4) << 14))
+
 namespace pi0 {
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {

@@ -56,8 +56,6 @@ struct TileArgs {
   int xcd_remap;
 };
 
-// vmcnt(n) with the other counters left alone (gfx9 encoding: vmcnt bits 3:0 and 15:14).
-#define PI0_VMCNT(n) (((n) & 0xF) | (0x7 << 4) | (0xF << 8) | (((n) >> 4) << 14))
 
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);

@@ -2,10 +2,12 @@
 //
 // Every decoder projection is C[M, N] = x[M, K] @ W[K, N] with M = 50 or 51:
 // the cost is streaming W from HBM once. One workgroup (4 waves) owns a
-// 16-column tile of W and a K range; each wave issues all of its weight loads
-// (16 bytes per lane, one contiguous 1 KB packed fragment per instruction)
-// before the first MFMA so that the whole slice is in flight at once. The
-// activation rows come from L2 as MFMA A fragments. Waves split K; their
+// 16-column tile of W and a K range; each wave issues all of its loads before
+// the first MFMA so that the whole slice is in flight at once: its activation
+// rows go from L2 straight into LDS (buffer loads with the LDS destination) in
+// 64-column k-blocks, each followed by that k-block's weight fragments (16 bytes
+// per lane, one contiguous 1 KB packed fragment per instruction), and the MFMAs
+// of a k-block wait only for the loads issued up to it. Waves split K; their
 // accumulators are summed in LDS. When the column tiles alone cannot fill the
 // chip (N = 1024), K is also split across workgroups: they store fp32 partial
 // tiles and a second launch (splitk_reduce_kernel) sums them in split order --
@@ -132,10 +134,15 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   constexpr int ND = DUAL ? 2 : 1;
   constexpr bool RMS = uses_rms(EPI);
   constexpr int KW = KTW * 32;            // k columns per wave
-  constexpr int XP = KW + 8;              // bf16 pitch of a staged x row (16 B pad: conflict-free reads)
-  constexpr int CHUNKS = KW / 8;          // 16-byte chunks per staged row
-  constexpr int XIT = (64 * CHUNKS) / PI0_WAVE;
-  constexpr size_t X_BYTES = 4 * 64 * XP * 2;
+  // x staging: k-blocks of KB k-tiles, k-block-major in LDS ([kb][64 rows][KB * 32])
+  constexpr int KB = KTW >= 2 ? 2 : 1;    // k-tiles per k-block
+  constexpr int NKB = KTW / KB;
+  constexpr int BCH = KB * 4;             // 16-byte chunks per row of a k-block
+  constexpr int XIB = BCH;                // load instructions per k-block (64 rows x 16 B x BCH)
+  constexpr int BRPI = PI0_WAVE / BCH;    // rows per load instruction
+  constexpr int OPS = XIB + KB * ND;      // vector-memory ops issued per k-block
+  static_assert(NKB <= 4 && 3 * OPS <= 63, "k-block waits");
+  constexpr size_t X_BYTES = 4 * 64 * KW * 2;
   constexpr size_t R_BYTES = (ND * 4 * 4 * 4 * PI0_WAVE + 4 * 4 * PI0_WAVE) * 4;
   __shared__ __attribute__((aligned(16))) char smem[X_BYTES > R_BYTES ? X_BYTES : R_BYTES];
 
@@ -148,39 +155,39 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   const int KT = a.K >> 5;
   const int kt0 = ks * (KT / splitk) + wave * KTW;
 
-  // ---- stage this wave's x slice [64 x KW] in LDS with coalesced 16-byte loads.
-  // The buffer resource ends after row `rows`: rows past M load as zeros.
-  __bf16* xs = reinterpret_cast<__bf16*>(smem) + wave * 64 * XP;
+  // 16-byte chunk c of row `row` of a k-block sits at chunk c ^ swz(row): the fragment
+  // reads of 8 consecutive rows then hit distinct banks
+  auto swz = [](int row) { return BCH == 8 ? (row & 7) : ((row >> 1) & 3); };
+  __bf16* xs = reinterpret_cast<__bf16*>(smem) + wave * 64 * KW;
   bf16x8 b0[KTW], b1[KTW];
   PI0_PROBE(0);
+  // ---- issue: this wave's x slice [64 x KW] goes straight from L2 into LDS (buffer
+  // loads with the LDS destination), one k-block at a time, each followed by the
+  // weight fragments of its k-tiles (cold, 16 bytes per lane, 1 KB per instruction).
+  // The scheduling barriers keep this order, which the k-block waits below count on.
+  // The buffer resource ends after row `rows`: rows past M arrive as zeros.
   {
-    constexpr int RPI = PI0_WAVE / CHUNKS;            // rows covered per load instruction
     const __amdgpu_buffer_rsrc_t xr =
         rows_rsrc(a.x + (size_t)m0 * a.ldx, rows * a.ldx * (int)sizeof(__bf16));
-    const int lrow0 = lane / CHUNKS, lch = lane % CHUNKS;
-    const int voff = (lrow0 * a.ldx + kt0 * 32 + lch * 8) * (int)sizeof(__bf16);
-    const int vstep = RPI * a.ldx * (int)sizeof(__bf16);
-    bf16x8 xv[XIT];
+    const int lrow0 = lane / BCH, lp = lane % BCH;
+    const __bf16* wp = a.w0 + ((size_t)nt * KT + kt0) * 512 + lane * 8;
+    const __bf16* wq = a.w1 + ((size_t)nt * KT + kt0) * 512 + lane * 8;
 #pragma unroll
-    for (int it = 0; it < XIT; ++it) xv[it] = buf_load8(xr, voff + it * vstep);
-    PI0_PROBE(1);
-    // weight stream, issued after the (L2-resident) x loads: loads return in
-    // order, so x is usable as soon as it lands and each MFMA waits only for
-    // the weight fragments it consumes. All fragments of the wave in flight.
-    {
-      const __bf16* wp = a.w0 + ((size_t)nt * KT + kt0) * 512 + lane * 8;
+    for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
-      for (int i = 0; i < KTW; ++i) b0[i] = load8(wp + i * 512);
-      if constexpr (DUAL) {
-        const __bf16* wq = a.w1 + ((size_t)nt * KT + kt0) * 512 + lane * 8;
-#pragma unroll
-        for (int i = 0; i < KTW; ++i) b1[i] = load8(wq + i * 512);
+      for (int q = 0; q < XIB; ++q) {
+        const int row = q * BRPI + lrow0, c = lp ^ swz(row);
+        buf_load16_lds(xr, xs + kb * 64 * KB * 32 + q * 512,
+                       (row * a.ldx + (kt0 + kb * KB) * 32 + c * 8) * (int)sizeof(__bf16));
       }
-    }
-    PI0_PROBE(2);
-    __bf16* xl = xs + lrow0 * XP + lch * 8;
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int it = 0; it < XIT; ++it) *reinterpret_cast<bf16x8*>(xl + it * RPI * XP) = xv[it];
+      for (int k2 = 0; k2 < KB; ++k2) {
+        b0[kb * KB + k2] = load8(wp + (kb * KB + k2) * 512);
+        if constexpr (DUAL) b1[kb * KB + k2] = load8(wq + (kb * KB + k2) * 512);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
   PI0_PROBE(3);
   // (each wave reads only the rows it staged itself: no workgroup barrier needed)
@@ -192,9 +199,24 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   float ssl[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < KTW; ++i) {
+    if (i % KB == 0) {
+      // k-block i / KB: memory operations complete in issue order, so once at most the
+      // later k-blocks' OPS each are outstanding, its x chunks are in LDS and its
+      // weight fragments in registers
+      __builtin_amdgcn_sched_barrier(0);
+      switch (NKB - 1 - i / KB) {   // folds to one s_waitcnt once the loop is unrolled
+        case 0: __builtin_amdgcn_s_waitcnt(PI0_VMCNT(0)); break;
+        case 1: __builtin_amdgcn_s_waitcnt(PI0_VMCNT(OPS)); break;
+        case 2: __builtin_amdgcn_s_waitcnt(PI0_VMCNT(2 * OPS)); break;
+        default: __builtin_amdgcn_s_waitcnt(PI0_VMCNT(3 * OPS)); break;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
-      const bf16x8 av = *reinterpret_cast<const bf16x8*>(xs + (mt * 16 + r) * XP + i * 32 + g * 8);
+      const int xrow = mt * 16 + r;
+      const bf16x8 av = *reinterpret_cast<const bf16x8*>(
+          xs + (i / KB) * 64 * KB * 32 + xrow * KB * 32 + ((((i % KB) * 4 + g) ^ swz(xrow)) * 8));
       acc0[mt] = mfma16(av, b0[i], acc0[mt]);
       if constexpr (DUAL) acc1[mt] = mfma16(av, b1[i], acc1[mt]);
       if constexpr (RMS) {       // sum of squares with v_dot2 (two bf16 products per op)

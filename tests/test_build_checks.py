@@ -1,0 +1,48 @@
+"""Device-code checks that run at build time (no GPU needed: hipcc cross-compiles).
+
+The skinny decoder GEMM stages its activation rows with buffer loads that write
+LDS directly; the wait before each k-block's MFMAs is correct only while the
+compiler keeps the issue order the source pins. build_lib.check_kblock_waits
+re-derives that from the generated assembly; these tests show it passes on the
+real kernels and rejects a wait that would let the MFMAs read LDS too early.
+"""
+import os
+import shutil
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, os.path.join(ROOT, "flash-vla_amd"))
+import build_lib  # noqa: E402
+
+pytestmark = pytest.mark.skipif(not os.path.exists(build_lib.HIPCC) and not shutil.which("hipcc"),
+                                reason="needs hipcc")
+
+
+@pytest.fixture(scope="module")
+def gemm_asm():
+    src = os.path.join(build_lib.CSRC, "pi0_gemm.hip")
+    res = subprocess.run([build_lib.HIPCC, *build_lib.FLAGS, "--cuda-device-only", "-S", src,
+                          "-o", "-"], capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+    return res.stdout
+
+
+def test_kblock_waits_hold(gemm_asm):
+    assert "skinny_gemm_kernel" in gemm_asm
+    assert build_lib.check_kblock_waits(gemm_asm) == []
+
+
+def test_kblock_waits_reject_a_loose_wait(gemm_asm):
+    name = "_ZN3pi018skinny_gemm_kernelILi4ELb1ELi8EEEvNS_8GemmArgsE"
+    start = gemm_asm.index(name + ":")
+    body = gemm_asm[start:gemm_asm.index("s_endpgm", start)]
+    first = body.index("s_waitcnt vmcnt(")
+    loose = body[:first] + "s_waitcnt vmcnt(60)" + body[body.index(")", first) + 1:]
+    assert build_lib.check_kblock_waits(gemm_asm.replace(body, loose)) == [name]
+
+
+def test_no_packed_fp32(gemm_asm):
+    assert not build_lib._PACKED_FP32.search(gemm_asm)
