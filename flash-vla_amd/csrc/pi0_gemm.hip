@@ -26,6 +26,11 @@
 namespace pi0 {
 
 constexpr int MAX_SPLITK = 8;
+#ifndef PI0_RED_THREADS
+#define PI0_RED_THREADS 64
+#endif
+// split-K second pass: threads per workgroup (4 per output row of a 16-column tile)
+constexpr int RED_THREADS = PI0_RED_THREADS;
 
 enum Epi { EPI_BIAS = 0, EPI_RES = 1, EPI_RMS_BIAS_RES = 2, EPI_QKV_ROPE = 3, EPI_GATE = 4 };
 
@@ -293,15 +298,19 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
 // count up to MAX_SPLITK. The residual of the EPI_RES call sites is loaded together
 // with the partials, so the kernel pays one memory round trip, not two.
 template <int EPI, bool DUAL, int SK>
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs a) {
+__global__ __launch_bounds__(RED_THREADS) void splitk_reduce_kernel(GemmArgs a) {
   constexpr int ND = DUAL ? 2 : 1;
   constexpr bool RMS = uses_rms(EPI);
   constexpr int NL = SK > 0 ? SK : MAX_SPLITK;
-  const int t = threadIdx.x, lrow = t >> 2, c4 = (t & 3) * 4;
-  const int nt = blockIdx.x, mb = blockIdx.y, ntiles = gridDim.x;
+  constexpr int QUARTERS = 256 / RED_THREADS;             // workgroups per 64-row tile
+  const int mb = blockIdx.y / QUARTERS;
+  const int t = threadIdx.x, lrow = (blockIdx.y % QUARTERS) * RED_THREADS / 4 + (t >> 2);
+  const int c4 = (t & 3) * 4;
+  const int nt = blockIdx.x, ntiles = gridDim.x;
   const int tile = mb * ntiles + nt, splitk = SK > 0 ? SK : a.splitk;
-  const size_t tiles = (size_t)gridDim.y * ntiles;
+  const size_t tiles = (size_t)(gridDim.y / QUARTERS) * ntiles;
   const int row = mb * 64 + lrow;
+  if (mb * 64 + (blockIdx.y % QUARTERS) * RED_THREADS / 4 >= a.M) return;   // padding rows only
   bf16x4 res4 = {};
   if constexpr (EPI == EPI_RES) {
     if (row < a.M) res4 = *reinterpret_cast<const bf16x4*>(a.out + (size_t)row * a.ldo + nt * 16 + c4);
@@ -357,12 +366,13 @@ static int launch_gemm(const GemmArgs& a, hipStream_t s) {
   }
   if (a.splitk > 1) {
     if (hipError_t e = hipGetLastError()) return (int)e;
-    const dim3 rgrid(a.N / 16, (a.M + 63) / 64);
+    const dim3 rgrid(a.N / 16, (a.M + 63) / 64 * (256 / RED_THREADS));
+    const dim3 rblock(RED_THREADS);
     switch (a.splitk) {
-      case 2: hipLaunchKernelGGL((splitk_reduce_kernel<EPI, DUAL, 2>), rgrid, dim3(256), 0, s, a); break;
-      case 4: hipLaunchKernelGGL((splitk_reduce_kernel<EPI, DUAL, 4>), rgrid, dim3(256), 0, s, a); break;
-      case 8: hipLaunchKernelGGL((splitk_reduce_kernel<EPI, DUAL, 8>), rgrid, dim3(256), 0, s, a); break;
-      default: hipLaunchKernelGGL((splitk_reduce_kernel<EPI, DUAL, 0>), rgrid, dim3(256), 0, s, a); break;
+      case 2: hipLaunchKernelGGL((splitk_reduce_kernel<EPI, DUAL, 2>), rgrid, rblock, 0, s, a); break;
+      case 4: hipLaunchKernelGGL((splitk_reduce_kernel<EPI, DUAL, 4>), rgrid, rblock, 0, s, a); break;
+      case 8: hipLaunchKernelGGL((splitk_reduce_kernel<EPI, DUAL, 8>), rgrid, rblock, 0, s, a); break;
+      default: hipLaunchKernelGGL((splitk_reduce_kernel<EPI, DUAL, 0>), rgrid, rblock, 0, s, a); break;
     }
   }
   return (int)hipGetLastError();
