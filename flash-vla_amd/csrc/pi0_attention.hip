@@ -232,10 +232,14 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
   }
 }
 
-// Second pass (several chunks): thread t of block b merges one 16-byte piece
-// (row (b*256 + t) / 64, columns 4*(t%64)..) over the chunks, in chunk order.
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-  const int id = blockIdx.x * 256 + threadIdx.x;
+// Second pass (several chunks): global thread id merges one 16-byte piece (row id / 64,
+// columns 4 (id % 64) ..) over the chunks, in chunk order.
+#ifndef PI0_CMB_THREADS
+#define PI0_CMB_THREADS 64
+#endif
+constexpr int CMB_THREADS = PI0_CMB_THREADS;     // merge threads per workgroup
+__global__ __launch_bounds__(CMB_THREADS) void attn_combine_kernel(AttnArgs a) {
+  const int id = blockIdx.x * CMB_THREADS + threadIdx.x;
   const int grow = id >> 6, col = (id & 63) * 4;
   if (grow >= a.rows * a.batch) return;
   const int bq = grow / a.rows, row = grow - bq * a.rows;
@@ -321,8 +325,8 @@ int pi0hip_attention_batched(const void* q, int ldq, const void* k, const void* 
   hipLaunchKernelGGL(attn_kernel, dim3(grid, batch), dim3(256), 0, s, a);
   if (a.nchunks > 1) {
     if (hipError_t e = hipGetLastError()) return (int)e;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((batch * rows * 64 + 255) / 256), dim3(256), 0, s,
-                       a);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((batch * rows * 64 + CMB_THREADS - 1) / CMB_THREADS),
+                       dim3(CMB_THREADS), 0, s, a);
   }
   return (int)hipGetLastError();
 }
