@@ -234,10 +234,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
 
 // Second pass (several chunks): global thread id merges one 16-byte piece (row id / 64,
 // columns 4 (id % 64) ..) over the chunks, in chunk order.
-#ifndef PI0_CMB_THREADS
-#define PI0_CMB_THREADS 64
-#endif
-constexpr int CMB_THREADS = PI0_CMB_THREADS;     // merge threads per workgroup
+constexpr int CMB_THREADS = 64;     // merge threads per workgroup (408 workgroups at config 2)
 __global__ __launch_bounds__(CMB_THREADS) void attn_combine_kernel(AttnArgs a) {
   const int id = blockIdx.x * CMB_THREADS + threadIdx.x;
   const int grow = id >> 6, col = (id & 63) * 4;

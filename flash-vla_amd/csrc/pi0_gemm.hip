@@ -26,11 +26,9 @@
 namespace pi0 {
 
 constexpr int MAX_SPLITK = 8;
-#ifndef PI0_RED_THREADS
-#define PI0_RED_THREADS 64
-#endif
-// split-K second pass: threads per workgroup (4 per output row of a 16-column tile)
-constexpr int RED_THREADS = PI0_RED_THREADS;
+// split-K second pass: threads per workgroup (4 per output row of a 16-column tile, so
+// 16 rows; one wave spreads the pass over 4x the CUs of a 64-row workgroup)
+constexpr int RED_THREADS = 64;
 
 enum Epi { EPI_BIAS = 0, EPI_RES = 1, EPI_RMS_BIAS_RES = 2, EPI_QKV_ROPE = 3, EPI_GATE = 4 };
 
