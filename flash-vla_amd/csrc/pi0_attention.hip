@@ -28,7 +28,8 @@ namespace pi0 {
 constexpr int ATT_HD = 256;
 constexpr int ATT_QT = 16;          // query rows per workgroup
 constexpr int ATT_CH = 128;         // keys per workgroup (32 per wave)
-constexpr int KP = ATT_HD + 8;      // bf16 pitch of staged K / V / Q rows
+constexpr int KP = ATT_HD + 8;      // bf16 pitch of staged K / Q rows
+constexpr int VP = ATT_HD + 16;     // bf16 pitch of staged V rows (544 B: 4 rows hit 4 bank groups)
 constexpr int OBP = ATT_HD + 4;     // fp32 pitch of the per-wave O buffer
 constexpr float NEG_BIG = -1.0e30f;
 constexpr int MAX_CHUNKS = 8;       // keys <= 1024
@@ -56,7 +57,7 @@ __device__ __forceinline__ int out_row(const AttnArgs& a, int b, int lr) {
 
 __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) __bf16 ks_[ATT_CH][KP];   // reused as O buffer
-  __shared__ __attribute__((aligned(16))) __bf16 vs_[ATT_CH][KP];
+  __shared__ __attribute__((aligned(16))) __bf16 vs_[ATT_CH][VP];
   __shared__ __attribute__((aligned(16))) __bf16 qs_[ATT_QT][KP];
   __shared__ float sm[4][ATT_QT], sl[4][ATT_QT];
 
@@ -151,17 +152,21 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
   for (int j = 0; j < 16; ++j) *reinterpret_cast<bf16x8*>(&vs_[row0 + 8 * j][ch * 8]) = vv[j];
   __syncthreads();
   PI0_PROBE(2);
-  // ---- O_w = P V_w : B fragment = V[keys kw + {4g..4g+3, 16+4g..16+4g+3}][column]
+  // ---- O_w = P V_w : B fragment = V[keys kw + {4g..4g+3, 16+4g..16+4g+3}][column].
+  // Each half comes from one transposing LDS read: within a 16-lane group, lane j slot
+  // k receives element j % 4 of the 8 bytes at lane 4k + j / 4's address, so lane
+  // 4k + c points at V[kw + 4g + k][16 dt + 4c .. +3] and lane r (column 16 dt + r)
+  // gets keys 4g .. 4g + 3 of its column.
   f32x4 o[16];
+  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+  const int vkey = kw + 4 * g + (r >> 2), vcol = (r & 3) * 4;
 #pragma unroll
   for (int dt = 0; dt < 16; ++dt) {
-    const int col = dt * 16 + r;
-    bf16x8 vf;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      vf[j] = vs_[kw + g * 4 + j][col];
-      vf[4 + j] = vs_[kw + 16 + g * 4 + j][col];
-    }
+    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+        (lds_bf16x4*)&vs_[vkey][dt * 16 + vcol]);
+    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+        (lds_bf16x4*)&vs_[vkey + 16][dt * 16 + vcol]);
+    const bf16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     o[dt] = mfma16(pf, vf, zero4());
   }
   PI0_PROBE(3);
