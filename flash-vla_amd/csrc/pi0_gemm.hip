@@ -346,10 +346,21 @@ __global__ __launch_bounds__(RED_THREADS) void splitk_reduce_kernel(GemmArgs a) 
   gemm_epilogue<EPI, DUAL>(a, row, nt, c4, (t & 3) == 0, v0, v1, ss);
 }
 
+// x rows are read (and copied into LDS) 16 bytes at a time; outputs are stored four
+// elements at a time (8 bytes, 16 for the fp32 Euler accumulator)
+static bool bad_alignment(const GemmArgs& a) {
+  const auto off = [](const void* p, uintptr_t m) { return (reinterpret_cast<uintptr_t>(p) & m) != 0; };
+  if (off(a.x, 15) || (a.ldx & 7) || a.ldx < a.K || (a.ldo & 3)) return true;
+  if (a.out_f32 ? off(a.out_f32, 15) : off(a.out, 7)) return true;
+  if (a.out_k && (off(a.out_k, 7) || off(a.out_v, 7) || (a.ldkv & 3))) return true;
+  return false;
+}
+
 template <int EPI, bool DUAL>
 static int launch_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0 || a.K <= 0) return PI0HIP_ERR_ARG;
   if (a.K % 32 || a.N % 16 || a.splitk < 1 || a.splitk > MAX_SPLITK) return PI0HIP_ERR_SHAPE;
+  if (bad_alignment(a)) return PI0HIP_ERR_SHAPE;
   const int KT = a.K / 32;
   if (KT % (4 * a.splitk)) return PI0HIP_ERR_SHAPE;
   if (a.splitk > 1 && !a.ws) return PI0HIP_ERR_WORKSPACE;

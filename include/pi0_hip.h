@@ -53,6 +53,13 @@ int pi0hip_small_linear(const void* x, int ldx, const void* w, const void* bias,
 int pi0hip_small_linear_f32x(const void* x, int ldx, const void* w, const void* bias, void* out,
                              int ldo, int M, int N, int K, int act, hipStream_t s);
 
+/* The skinny GEMMs below (pi0hip_linear_bias, pi0hip_linear_residual,
+ * pi0hip_rms_linear_bias_residual[_f32], pi0hip_norm_qkv_rope[_batched],
+ * pi0hip_norm_gated_ffn) read x rows 16 bytes at a time and store four outputs
+ * at a time: x 16-byte aligned with ldx % 8 == 0 and ldx >= K; out (and K / V)
+ * 8-byte aligned (16 for the fp32 accumulator) with ldo (ldkv) % 4 == 0;
+ * otherwise PI0HIP_ERR_SHAPE. */
+
 /* out = x @ W + bias, fp32 accumulation, M <= 64 per 64-row block.
  * decoder_action_mlp wrappers.py:123-128 (tl_matmul_bias, kernels/base.py:158-192) */
 int pi0hip_linear_bias(const void* x, int ldx, const void* w_packed, const void* bias, void* out,

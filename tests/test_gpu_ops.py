@@ -204,3 +204,26 @@ def test_layer_views_of_a_stacked_weight():
         close(out, O.op_matmul_residual(x.float(), ws[i].cpu().float(), torch.zeros(51, 1024)),
               what=f"layer {i}")
 
+
+
+def test_skinny_gemm_rejects_misaligned_operands():
+    """The skinny GEMMs read x rows 16 bytes at a time (straight into LDS) and store four
+    outputs at a time: a row pitch that is not a multiple of 8 elements, a pitch below K,
+    or an x pointer off a 16-byte boundary is a shape error, raised before any launch."""
+    from flash_vla_amd.backends.hip import _abi
+    lib = _abi.lib()
+    M, K, N = 51, 1024, 1024
+    x = torch.zeros((M, K + 8), dtype=torch.bfloat16, device=DEV)
+    wp = torch.zeros((K, N), dtype=torch.bfloat16, device=DEV)
+    out = torch.zeros((M, N), dtype=torch.bfloat16, device=DEV)
+    s = torch.cuda.current_stream().cuda_stream
+
+    def run(xptr, ldx):
+        return lib.pi0hip_linear_residual(xptr, ldx, wp.data_ptr(), out.data_ptr(), N, M, N, K,
+                                          1, None, 0, s)
+
+    assert run(x.data_ptr(), K + 8) == 0
+    torch.cuda.synchronize()
+    assert run(x.data_ptr(), K + 4) == -2            # pitch not a multiple of 8
+    assert run(x.data_ptr(), K - 8) == -2            # pitch below K
+    assert run(x.data_ptr() + 8, K + 8) == -2        # x not 16-byte aligned
