@@ -55,10 +55,14 @@ __device__ __forceinline__ int out_row(const AttnArgs& a, int b, int lr) {
   return tok * a.heads + head;
 }
 
-__global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) __bf16 ks_[ATT_CH][KP];   // reused as O buffer
-  __shared__ __attribute__((aligned(16))) __bf16 vs_[ATT_CH][VP];
+__global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
+  // One LDS area holds K (pitch KP) for S, then V (pitch VP) for P @ V, then the fp32
+  // per-wave O buffer: ~79 KB in all, so two workgroups fit on a CU (batched requests).
+  __shared__ __attribute__((aligned(16))) __bf16 kv_[ATT_CH * VP];
   __shared__ __attribute__((aligned(16))) __bf16 qs_[ATT_QT][KP];
+  auto ks_ = reinterpret_cast<__bf16 (*)[KP]>(kv_);
+  auto vs_ = reinterpret_cast<__bf16 (*)[VP]>(kv_);
+  static_assert(4 * ATT_QT * OBP * sizeof(float) <= sizeof(kv_), "O buffer");
   __shared__ float sm[4][ATT_QT], sl[4][ATT_QT];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -147,6 +151,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
   lsum += __shfl_xor(lsum, 32, PI0_WAVE);
   if (g == 0) { sm[wave][r] = mx; sl[wave][r] = lsum; }
 
+  __syncthreads();          // every wave is done reading K: V takes its place
   // ---- publish V (its loads were in flight during S and the softmax)
 #pragma unroll
   for (int j = 0; j < 16; ++j) *reinterpret_cast<bf16x8*>(&vs_[row0 + 8 * j][ch * 8]) = vv[j];
@@ -170,7 +175,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
     o[dt] = mfma16(pf, vf, zero4());
   }
   PI0_PROBE(3);
-  __syncthreads();          // sm/sl complete; every wave is done reading ks_
+  __syncthreads();          // every wave is done reading V
 
   // ---- merge the 4 waves: O = sum_w 2^(m_w - M) O_w (rows 4g+i of this lane)
   float alpha[4];
@@ -182,7 +187,7 @@ __global__ __launch_bounds__(256, 1) void attn_kernel(AttnArgs a) {
     for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w][qr]);
     alpha[i] = fast_exp2(sm[wave][qr] - M);   // 0 for an empty wave next to a non-empty one
   }
-  float* ob = reinterpret_cast<float*>(&ks_[0][0]);      // [4][16][OBP] fp32
+  float* ob = reinterpret_cast<float*>(kv_);             // [4][16][OBP] fp32
 #pragma unroll
   for (int dt = 0; dt < 16; ++dt)
 #pragma unroll
