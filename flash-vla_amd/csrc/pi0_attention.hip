@@ -193,29 +193,31 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       ob[(wave * ATT_QT + g * 4 + i) * OBP + dt * 16 + r] = o[dt][i] * alpha[i];
+  // the merged rows' 1 / L and log2-sum-exp, once per row (threads 0..15)
+  __shared__ float rinv[ATT_QT], rlse[ATT_QT];
+  if (t < ATT_QT) {
+    float M = NEG_BIG;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w][t]);
+    // branch-free: an empty wave has m_w = NEG_BIG and l_w = 0, so its term is 0
+    float L = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) L += fast_exp2(sm[w][t] - M) * sl[w][t];
+    rinv[t] = L > 0.f ? __builtin_amdgcn_rcpf(L) : 0.f;
+    rlse[t] = L > 0.f ? M + __builtin_amdgcn_logf(L) : NEG_BIG;
+  }
   __syncthreads();
 
   PI0_PROBE(4);
   // thread t owns 4 16-byte pieces: piece id = t + 256 j -> row id/64, columns 4*(id%64)..
   f32x4 acc[4];
-  float rowM[4], rowL[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int id = t + 256 * j, row = id >> 6, col = (id & 63) * 4;
-    float M = NEG_BIG;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w][row]);
-    // branch-free: an empty wave has m_w = NEG_BIG and l_w = 0, so its term is 0
-    float L = 0.f;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) L += fast_exp2(sm[w][row] - M) * sl[w][row];
     f32x4 v = zero4();
 #pragma unroll
     for (int w = 0; w < 4; ++w) v += *reinterpret_cast<const f32x4*>(&ob[(w * ATT_QT + row) * OBP + col]);
-    const float inv = L > 0.f ? __builtin_amdgcn_rcpf(L) : 0.f;
-    acc[j] = v * inv;
-    rowM[j] = M;
-    rowL[j] = L;
+    acc[j] = v * rinv[row];
   }
 
   if (a.nchunks == 1) {
@@ -236,9 +238,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   for (int j = 0; j < 4; ++j) {
     const int id = t + 256 * j, prow = q0 + (id >> 6), col = (id & 63) * 4;
     *reinterpret_cast<f32x4*>(a.part + ((size_t)c * a.rows_pad + prow) * ATT_HD + col) = acc[j];
-    if ((id & 63) == 0)
-      a.lse[(size_t)c * a.rows_pad + prow] =
-          rowL[j] > 0.f ? rowM[j] + __builtin_amdgcn_logf(rowL[j]) : NEG_BIG;
+    if ((id & 63) == 0) a.lse[(size_t)c * a.rows_pad + prow] = rlse[id >> 6];
   }
 }
 
