@@ -72,15 +72,30 @@ def check_kblock_waits(asm: str) -> list[str]:
     return bad
 
 
+def scratch_kernels(asm: str) -> list[str]:
+    """Kernels whose private (scratch) segment is not empty: a spill, or a kernel argument
+    indexed at run time and so copied to the stack -- both silent slowdowns."""
+    bad = []
+    for m in re.finditer(r"^\s*\.amdhsa_kernel\s+(\S+)(.*?)^\s*\.end_amdhsa_kernel", asm, re.M | re.S):
+        size = re.search(r"\.amdhsa_private_segment_fixed_size\s+(\d+)", m.group(2))
+        if size and int(size.group(1)) > 0:
+            bad.append(m.group(1))
+    return bad
+
+
 def check_device_code(src: str) -> None:
     """Compile `src` to device assembly and fail if any packed fp32 VALU op was
-    generated, or (pi0_gemm.hip) if a skinny GEMM's k-block waits are unsafe."""
+    generated, if any kernel uses scratch memory, or (pi0_gemm.hip) if a skinny GEMM's
+    k-block waits are unsafe."""
     cmd = [HIPCC, *FLAGS, "--cuda-device-only", "-S", src, "-o", "-"]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc -S failed for {src}:\n{res.stderr}")
     if _PACKED_FP32.search(res.stdout):
         raise RuntimeError(f"{src}: packed fp32 VALU instructions in the device code")
+    scratch = scratch_kernels(res.stdout)
+    if scratch:
+        raise RuntimeError(f"{src}: kernels with a scratch segment: {scratch}")
     if os.path.basename(src) == "pi0_gemm.hip":
         bad = check_kblock_waits(res.stdout)
         if bad:

@@ -33,6 +33,7 @@ constexpr int VP = ATT_HD + 16;     // bf16 pitch of staged V rows (544 B: 4 row
 constexpr int OBP = ATT_HD + 4;     // fp32 pitch of the per-wave O buffer
 constexpr float NEG_BIG = -1.0e30f;
 constexpr int MAX_CHUNKS = 8;       // keys <= 1024
+constexpr int PF_MAX = 3;           // prefetch regions
 
 struct AttnArgs {
   const __bf16* q; int ldq;
@@ -43,7 +44,38 @@ struct AttnArgs {
   float scale_log2;
   int batch;                 // requests (grid.y); request b reads K / V at b * kv_bstride
   long long kv_bstride;
+  // optional L2 prefetch by spare workgroups (blockIdx.x >= work_grid, batch 1):
+  // region r is pf_nslices[r] slices of pf_slice_words[r] dwords; slice s is what
+  // workgroup s of the launch that consumes it reads, so it runs on XCD s % 8
+  int work_grid, pf_workgroups, pf_n;
+  const unsigned* pf_base[PF_MAX];
+  int pf_slice_words[PF_MAX], pf_nslices[PF_MAX];
 };
+
+// Spare workgroup: touch one dword of every 128-byte line of the slices that will be
+// read on this workgroup's XCD (workgroup b of a launch runs on XCD b % 8), pulling
+// them into that XCD's L2 while the attention runs on the other CUs. Loads only;
+// the sum is kept alive by an empty asm statement, nothing is stored.
+__device__ __forceinline__ void prefetch_slices(const AttnArgs& a) {
+  const int p = blockIdx.x, x = p & 7, t = threadIdx.x;
+  const int k0 = (x - a.work_grid % 8 + 8) % 8;          // first spare workgroup on XCD x
+  if (a.pf_workgroups <= k0) return;
+  const int j = (p - a.work_grid - k0) / 8;             // its index there ...
+  const int per_xcd = (a.pf_workgroups - k0 + 7) / 8;   // ... and their number
+  unsigned acc = 0;
+#pragma unroll
+  for (int r = 0; r < PF_MAX; ++r) {     // constant indices: the argument arrays stay in SGPRs
+    if (r >= a.pf_n) break;
+    const int lines = a.pf_slice_words[r] / 32;
+    const int items = (a.pf_nslices[r] - x + 7) / 8 * lines;
+    const unsigned* base = a.pf_base[r];
+    for (int it = j * 256 + t; it < items; it += per_xcd * 256) {
+      const int sl = x + 8 * (it / lines), l = it - (it / lines) * lines;
+      acc += base[(size_t)sl * a.pf_slice_words[r] + l * 32];
+    }
+  }
+  asm volatile("" ::"v"(acc));
+}
 
 // Output row of local flat row lr (= token * heads + head) of request b: the tokens of a
 // batch are stored "states first" (B state tokens, then B x T action tokens), the order
@@ -65,6 +97,10 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   static_assert(4 * ATT_QT * OBP * sizeof(float) <= sizeof(kv_), "O buffer");
   __shared__ float sm[4][ATT_QT], sl[4][ATT_QT];
 
+  if ((int)blockIdx.x >= a.work_grid) {
+    prefetch_slices(a);
+    return;
+  }
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int qt = blockIdx.x % a.nqt, c = blockIdx.x / a.nqt;
@@ -285,25 +321,28 @@ using namespace pi0;
 
 static inline size_t round256(size_t v) { return (v + 255) / 256 * 256; }
 
-extern "C" {
+extern "C" size_t pi0hip_attention_batched_workspace_bytes(int rows, int keys, int batch);
 
-size_t pi0hip_attention_batched_workspace_bytes(int rows, int keys, int batch) {
-  if (rows <= 0 || keys <= 0 || batch <= 0) return 0;
-  const size_t nch = (size_t)(keys + ATT_CH - 1) / ATT_CH;
-  const size_t nqt = (size_t)(rows + ATT_QT - 1) / ATT_QT;
-  const size_t rows_pad = nqt * ATT_QT;
-  return round256((size_t)batch * nch * rows_pad * sizeof(float)) +
-         (size_t)batch * nch * rows_pad * ATT_HD * sizeof(float);
+// CUs of the current device (cached per device): the prefetch fills the chip to two
+// workgroups per CU, the attention kernel's occupancy.
+static int device_cus() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
 }
 
-size_t pi0hip_attention_workspace_bytes(int rows, int keys) {
-  return pi0hip_attention_batched_workspace_bytes(rows, keys, 1);
-}
-
-int pi0hip_attention_batched(const void* q, int ldq, const void* k, const void* v, int ldkv,
-                             long long kv_bstride, void* out, int ldo, int rows, int keys,
-                             int enc_len, int heads, int head_dim, int batch, void* ws,
-                             size_t ws_bytes, hipStream_t s) {
+static int attention_launch(const void* q, int ldq, const void* k, const void* v, int ldkv,
+                            long long kv_bstride, void* out, int ldo, int rows, int keys,
+                            int enc_len, int heads, int head_dim, int batch, void* ws,
+                            size_t ws_bytes, int npf, const void* const* pf_ptr,
+                            const size_t* pf_bytes, const int* pf_slices, hipStream_t s) {
   if (!q || !k || !v || !out || rows <= 0 || keys <= 0 || batch <= 0 || heads <= 0)
     return PI0HIP_ERR_ARG;
   if (head_dim != ATT_HD || keys > MAX_CHUNKS * ATT_CH || (batch > 1 && rows % heads))
@@ -324,18 +363,68 @@ int pi0hip_attention_batched(const void* q, int ldq, const void* k, const void* 
   a.rows_pad = nqt * ATT_QT;
   a.nqt = nqt;
   const int grid = nqt * a.nchunks;
+  a.work_grid = grid;
+  for (int r = 0; r < npf; ++r) {          // prefetch regions (null pointers are skipped)
+    if (!pf_ptr[r]) continue;
+    const size_t b = pf_bytes[r];
+    const int n = pf_slices[r];
+    if (n <= 0 || b == 0 || b % n || (b / n) % 128 || b / n / 4 > (size_t)INT32_MAX ||
+        (reinterpret_cast<uintptr_t>(pf_ptr[r]) & 3))
+      return PI0HIP_ERR_SHAPE;
+    a.pf_base[a.pf_n] = static_cast<const unsigned*>(pf_ptr[r]);
+    a.pf_slice_words[a.pf_n] = static_cast<int>(b / n / 4);
+    a.pf_nslices[a.pf_n] = n;
+    ++a.pf_n;
+  }
+  a.pf_workgroups = a.pf_n ? max(0, 2 * device_cus() - grid) : 0;
   char* base = reinterpret_cast<char*>(ws);
   a.lse = reinterpret_cast<float*>(base);
   base += round256((size_t)batch * a.nchunks * a.rows_pad * sizeof(float));
   a.part = reinterpret_cast<float*>(base);
   a.scale_log2 = 1.4426950408889634f / sqrtf((float)head_dim);
-  hipLaunchKernelGGL(attn_kernel, dim3(grid, batch), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(attn_kernel, dim3(grid + a.pf_workgroups, batch), dim3(256), 0, s, a);
   if (a.nchunks > 1) {
     if (hipError_t e = hipGetLastError()) return (int)e;
     hipLaunchKernelGGL(attn_combine_kernel, dim3((batch * rows * 64 + CMB_THREADS - 1) / CMB_THREADS),
                        dim3(CMB_THREADS), 0, s, a);
   }
   return (int)hipGetLastError();
+}
+
+extern "C" {
+
+size_t pi0hip_attention_batched_workspace_bytes(int rows, int keys, int batch) {
+  if (rows <= 0 || keys <= 0 || batch <= 0) return 0;
+  const size_t nch = (size_t)(keys + ATT_CH - 1) / ATT_CH;
+  const size_t nqt = (size_t)(rows + ATT_QT - 1) / ATT_QT;
+  const size_t rows_pad = nqt * ATT_QT;
+  return round256((size_t)batch * nch * rows_pad * sizeof(float)) +
+         (size_t)batch * nch * rows_pad * ATT_HD * sizeof(float);
+}
+
+size_t pi0hip_attention_workspace_bytes(int rows, int keys) {
+  return pi0hip_attention_batched_workspace_bytes(rows, keys, 1);
+}
+
+int pi0hip_attention_batched(const void* q, int ldq, const void* k, const void* v, int ldkv,
+                             long long kv_bstride, void* out, int ldo, int rows, int keys,
+                             int enc_len, int heads, int head_dim, int batch, void* ws,
+                             size_t ws_bytes, hipStream_t s) {
+  return attention_launch(q, ldq, k, v, ldkv, kv_bstride, out, ldo, rows, keys, enc_len, heads,
+                          head_dim, batch, ws, ws_bytes, 0, nullptr, nullptr, nullptr, s);
+}
+
+int pi0hip_attention_prefetch(const void* q, int ldq, const void* k, const void* v, int ldkv,
+                              void* out, int ldo, int rows, int keys, int enc_len, int heads,
+                              int head_dim, void* ws, size_t ws_bytes, const void* pf0,
+                              size_t pf0_bytes, int pf0_slices, const void* pf1, size_t pf1_bytes,
+                              int pf1_slices, const void* pf2, size_t pf2_bytes, int pf2_slices,
+                              hipStream_t s) {
+  const void* ptr[PF_MAX] = {pf0, pf1, pf2};
+  const size_t bytes[PF_MAX] = {pf0_bytes, pf1_bytes, pf2_bytes};
+  const int slices[PF_MAX] = {pf0_slices, pf1_slices, pf2_slices};
+  return attention_launch(q, ldq, k, v, ldkv, 0, out, ldo, rows, keys, enc_len, heads, head_dim,
+                          1, ws, ws_bytes, PF_MAX, ptr, bytes, slices, s);
 }
 
 int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int ldkv, void* out,

@@ -41,6 +41,9 @@ PROTOTYPES = {
     "pi0hip_attention_batched_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "pi0hip_attention_batched": (c_int, [P, c_int, P, P, c_int, ctypes.c_longlong, P, c_int, c_int,
                                          c_int, c_int, c_int, c_int, c_int, P, c_size_t, P]),
+    "pi0hip_attention_prefetch": (c_int, [P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int,
+                                          c_int, c_int, P, c_size_t, P, c_size_t, c_int, P,
+                                          c_size_t, c_int, P, c_size_t, c_int, P]),
     "pi0hip_tile_qkv_rope_batched": (c_int, [P, c_int, P, P, P, P, P, c_int, ctypes.c_longlong,
                                              c_int, c_int, c_int, c_int, c_int, P]),
     "pi0hip_encoder_attention_batched_workspace_bytes": (c_size_t, [c_int, c_int]),

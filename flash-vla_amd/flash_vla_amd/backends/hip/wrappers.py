@@ -283,6 +283,43 @@ def decoder_attention(Q, K, V, scores, out, encoder_seq_len):
     return out
 
 
+def decoder_attention_prefetch(Q, K, V, scores, out, encoder_seq_len, gate_w, up_w, down_w):
+    """`decoder_attention` whose spare workgroups also pull this layer's gate / up / down
+    weights into the L2 of the XCDs that will read them (pi0hip_attention_prefetch).
+
+    Engine-level option of this backend, not a reference call site: the reference's
+    decoder_attention (fused_wrappers.py:88-115) prefetches nothing. The result is bitwise
+    that of decoder_attention. Used for one request whose GEMMs take the skinny kernels,
+    where workgroup s of the gate / up launch reads packed tile s and workgroup s of the
+    split-K down launch reads the s-th of its (N / 16) x splitk K-slices; otherwise it
+    is plain decoder_attention."""
+    rows = Q.shape[0]
+    M = rows // DECODER_HEADS
+    if K.dim() == 3 or M > _TILE_M:
+        return decoder_attention(Q, K, V, scores, out, encoder_seq_len)
+    _check(Q, "Q", 2); _check(out, "out", 2); _check(K, "K", 2); _check(V, "V", 2)
+    keys, head_dim = K.shape
+    if (V.shape != K.shape or head_dim != Q.shape[1] or out.shape != Q.shape
+            or K.stride(0) != V.stride(0)):
+        raise ValueError("decoder_attention: shape mismatch")
+    regions = []
+    for w, splitk in ((gate_w, 1), (up_w, 1), (down_w, 0)):     # 0: the down's split-K count
+        Kw, Nw = w.shape
+        regions += [packed_weight_ptr(w), Kw * Nw * 2, (Nw // 16) * (splitk or _splitk(M, Nw, Kw))]
+    lib = _abi.lib()
+    nbytes = lib.pi0hip_attention_batched_workspace_bytes(rows, keys, 1)
+    ws = scratch("attn_ws", (nbytes,), torch.uint8, Q.device)
+    _abi.call("pi0hip_attention_prefetch", _ptr(Q), Q.stride(0), _ptr(K), _ptr(V), K.stride(0),
+              _ptr(out), out.stride(0), rows, keys, int(encoder_seq_len), DECODER_HEADS, head_dim,
+              ws.data_ptr(), nbytes, *regions, _stream())
+    return out
+
+
+def attention_prefetch_for(attention_op):
+    """The prefetching form of `attention_op` if it is this backend's decoder_attention."""
+    return decoder_attention_prefetch if attention_op is decoder_attention else None
+
+
 # Above one 64-row block (the batched decoder, M = B x 51) the decoder's GEMMs run on the
 # prefix encoder's tile kernel: the skinny kernel would stream the weights once per row block.
 _TILE_M = 64

@@ -23,22 +23,33 @@ from .ops import op_table
 from .spec import DECODER_WEIGHT_NAMES, decoder_weight_shapes, weight_shapes
 
 
+def _attention_prefetch(backend, ops, enabled: bool):
+    """The backend's prefetching form of the table's decoder_attention, if it has one
+    (the table entry itself is left untouched, so a plan that routes decoder_attention
+    elsewhere gets no prefetch)."""
+    pick = getattr(backend, "attention_prefetch_for", None)
+    return pick(ops.decoder_attention) if enabled and pick is not None else None
+
+
 class Pi0DecoderEngine:
     """The captured 10-step decoder loop against a caller-supplied prefix KV cache.
 
-    steps and layers exist for bisection, as in the reference engine.
+    steps and layers exist for bisection, as in the reference engine. With `prefetch`
+    (default) and a backend that offers it, each layer's attention launch also pulls the
+    layer's FFN weights into L2 (same results; see `backends.hip.attention_prefetch_for`).
     """
 
     def __init__(self, weights: dict, encoder_seq_len: int = 768, chunk_size: int = 50,
                  steps: int = 10, layers: int = 18, fused: bool = True, backend: str = "hip",
                  plan: dict | None = None, device: str = "cuda", capture: bool = True,
-                 warmup: int = 3, fp32_euler: bool = True):
+                 warmup: int = 3, fp32_euler: bool = True, prefetch: bool = True):
         self.encoder_seq_len = encoder_seq_len
         self.chunk_size = chunk_size
         self.steps = steps
         self.layers = layers
         self.ops = op_table(fused, backend=backend, plan=plan)
         self.backend = BACKENDS[backend]
+        self.attention_prefetch = _attention_prefetch(self.backend, self.ops, prefetch)
         n_layers = weights["decoder_attn_qkv_w"].shape[0]
         if layers > n_layers:
             raise ValueError(f"layers={layers} but the checkpoint has {n_layers}")
@@ -70,7 +81,8 @@ class Pi0DecoderEngine:
         with self.backend.use_pool(self.pool):
             pipeline.transformer_decoder(self.ops, self.weights, self.buffers,
                                          self.encoder_seq_len, steps=self.steps,
-                                         layers=self.layers)
+                                         layers=self.layers,
+                                         attention_prefetch=self.attention_prefetch)
 
     def _capture(self, warmup: int):
         saved = self.buffers["diffusion_noise"].clone()
@@ -202,7 +214,8 @@ class Pi0Inference:
                  steps: int = 10, layers: int = 18, fused: bool = True, device: str = "cuda",
                  backend: str = "hip", plan: dict | None = None, fp32_euler: bool = True,
                  vision_layers: int | None = None, encoder_layers: int | None = None,
-                 capture: bool = True, warmup: int = 3, batch: int = 1, prompt_tokens: int = 0):
+                 capture: bool = True, warmup: int = 3, batch: int = 1, prompt_tokens: int = 0,
+                 prefetch: bool = True):
         """batch > 1 and prompt_tokens > 0 are the BASELINE config-5 profile (not in the
         reference, which is batch-1 with precomputed `language_embeds`): B independent
         requests share every GEMM, and each request's prompt is `prompt_tokens` token ids
@@ -217,6 +230,7 @@ class Pi0Inference:
         self.encoder_layers = encoder_layers
         self.ops = op_table(fused, backend=backend, plan=plan)
         self.backend = BACKENDS[backend]
+        self.attention_prefetch = _attention_prefetch(self.backend, self.ops, prefetch)
         self.prompt_len = prompt_tokens if prompt_tokens else len(checkpoint["language_embeds"])
         bf16 = torch.bfloat16
         shapes = weight_shapes(self.prompt_len)
@@ -270,7 +284,8 @@ class Pi0Inference:
             pipeline.transformer_encoder(self.ops, self.weights, b, self.encoder_seq_len,
                                          layers=self.encoder_layers)
             pipeline.transformer_decoder(self.ops, self.weights, b, self.encoder_seq_len,
-                                         steps=self.steps, layers=self.layers)
+                                         steps=self.steps, layers=self.layers,
+                                         attention_prefetch=self.attention_prefetch)
 
     def _capture(self, warmup: int):
         saved = self.buffers["diffusion_noise"].clone()

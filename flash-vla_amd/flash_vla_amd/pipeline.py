@@ -106,7 +106,8 @@ def transformer_encoder(ops, weights, buffers, encoder_seq_len, layers=None, pro
             buffers["encoder_hidden"], weights["encoder_ffn_down_w"][i], buffers["encoder_x"])
 
 
-def transformer_decoder(ops, weights, buffers, encoder_seq_len, steps=10, layers=18):
+def transformer_decoder(ops, weights, buffers, encoder_seq_len, steps=10, layers=18,
+                        attention_prefetch=None):
     B = _batch(buffers)
     ops.decoder_state_proj(
         buffers["observation_state_normalized"], weights["decoder_state_in_proj_w"],
@@ -130,10 +131,14 @@ def transformer_decoder(ops, weights, buffers, encoder_seq_len, steps=10, layers
                 _layer_cache(buffers, "encoder_K", i, dec_rows),
                 _layer_cache(buffers, "encoder_V", i, dec_rows),
                 buffers["decoder_norm_factor_buf"])
-            ops.decoder_attention(
-                buffers["decoder_q_buf"], _layer_cache(buffers, "encoder_K", i),
-                _layer_cache(buffers, "encoder_V", i),
-                buffers["decoder_attn_buf"], buffers["decoder_q_buf"], encoder_seq_len)
+            attn_args = (buffers["decoder_q_buf"], _layer_cache(buffers, "encoder_K", i),
+                         _layer_cache(buffers, "encoder_V", i),
+                         buffers["decoder_attn_buf"], buffers["decoder_q_buf"], encoder_seq_len)
+            if attention_prefetch is None:
+                ops.decoder_attention(*attn_args)
+            else:   # same result; also pulls this layer's FFN weights into L2
+                attention_prefetch(*attn_args, weights["decoder_ffn_gate_w"][i],
+                                   weights["decoder_ffn_up_w"][i], weights["decoder_ffn_down_w"][i])
             ops.decoder_out_proj_residual(
                 buffers["decoder_q_buf"].view(buffers["decoder_x"].shape[0], -1), weights["decoder_attn_o_w"][i],
                 buffers["decoder_x"])

@@ -46,3 +46,19 @@ def test_kblock_waits_reject_a_loose_wait(gemm_asm):
 
 def test_no_packed_fp32(gemm_asm):
     assert not build_lib._PACKED_FP32.search(gemm_asm)
+
+
+def test_no_kernel_uses_scratch():
+    """Every kernel runs without a scratch segment: a runtime-indexed kernel argument
+    (copied to the stack) or a register spill shows up here before it shows up as a
+    slowdown on the GPU."""
+    src = os.path.join(build_lib.CSRC, "pi0_attention.hip")
+    res = subprocess.run([build_lib.HIPCC, *build_lib.FLAGS, "--cuda-device-only", "-S", src,
+                          "-o", "-"], capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+    assert "attn_kernel" in res.stdout
+    assert build_lib.scratch_kernels(res.stdout) == []
+    fake = ("\t.amdhsa_kernel k_spills\n\t\t.amdhsa_private_segment_fixed_size 192\n"
+            "\t.end_amdhsa_kernel\n\t.amdhsa_kernel k_clean\n"
+            "\t\t.amdhsa_private_segment_fixed_size 0\n\t.end_amdhsa_kernel\n")
+    assert build_lib.scratch_kernels(fake) == ["k_spills"]

@@ -141,3 +141,17 @@ def test_ten_steps_more_seeds(seed):
           f"(bf16 emulation mean {mean_emu:.2e})")
     assert err <= 2e-2 and cos >= 0.999
     assert mean_gpu <= mean_emu
+
+
+def test_prefetch_does_not_change_the_chunk(case):
+    """The engine's attention-launch prefetch of each layer's FFN weights leaves the
+    captured 10-step chunk bitwise unchanged."""
+    ck, inp = case
+    outs = []
+    for prefetch in (True, False):
+        eng = Pi0DecoderEngine({k: v.to(DEV) for k, v in ck.items()}, prefetch=prefetch)
+        assert (eng.attention_prefetch is not None) == prefetch
+        eng.load_prefix(inp["encoder_K"].to(DEV), inp["encoder_V"].to(DEV))
+        outs.append(eng.forward(inp["observation_state_normalized"].to(DEV),
+                                inp["diffusion_noise"].to(DEV)).clone())
+    assert torch.equal(outs[0], outs[1])

@@ -227,3 +227,22 @@ def test_skinny_gemm_rejects_misaligned_operands():
     assert run(x.data_ptr(), K + 4) == -2            # pitch not a multiple of 8
     assert run(x.data_ptr(), K - 8) == -2            # pitch below K
     assert run(x.data_ptr() + 8, K + 8) == -2        # x not 16-byte aligned
+
+
+def test_attention_prefetch_is_bitwise_attention():
+    """The prefetching attention (spare workgroups pull the layer's gate / up / down
+    weights into L2) returns exactly what decoder_attention returns."""
+    rows, keys, enc = 408, 819, 768
+    q = rnd((rows, 256), 31).to(DEV)
+    k = rnd((keys, 256), 32).to(DEV)
+    v = rnd((keys, 256), 33).to(DEV)
+    gate = rnd((1024, 4096), 34, 0.02).to(DEV)
+    up = rnd((1024, 4096), 35, 0.02).to(DEV)
+    down = rnd((4096, 1024), 36, 0.02).to(DEV)
+    ref = W.decoder_attention(q.clone(), k, v, None, q.clone(), enc)
+    out = torch.empty_like(q)
+    got = W.decoder_attention_prefetch(q.clone(), k, v, None, out, enc, gate, up, down)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    assert W.attention_prefetch_for(W.decoder_attention) is W.decoder_attention_prefetch
+    assert W.attention_prefetch_for(W.decoder_norm_gated_ffn) is None
