@@ -85,6 +85,12 @@ __device__ __forceinline__ void buf_load16_lds(__amdgpu_buffer_rsrc_t r, void* l
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base,
                                            16, off, 0, 0, 0);
 }
+// The same with a wave-uniform byte offset `soff` (an SGPR) added to the lane offset.
+__device__ __forceinline__ void buf_load16_lds_s(__amdgpu_buffer_rsrc_t r, void* lds_base, int off,
+                                                 int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base,
+                                           16, off, __builtin_amdgcn_readfirstlane(soff), 0, 0);
+}
 __device__ __forceinline__ bf16x8 buf_load8(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }

@@ -311,6 +311,142 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
   }
 }
 
+// ---- gated FFN on a wave grid, both operands staged in LDS ---------------------------
+// Workgroup = NW waves as (NW / 2) x 2: BM rows x 256 packed B columns (128 gate + the
+// matching 128 up), i.e. 128 output columns; wave (wm, wn) owns BM / (NW / 2) rows and
+// output columns wn * 64 .. + 64 (gate tiles 2 wn, 2 wn + 1 and the same up tiles). Per
+// 64-deep step a 384-row block loads 384 + 256 rows of 128 bytes for 384 x 256 x 64 MACs,
+// against 2 x (128 + 256) rows for 2 x 128 x 256 x 64 in the two-per-CU strip kernel
+// above, whose weight stream into VGPRs saturates the per-CU load path. Both operands go
+// global -> LDS directly (buffer_load ... lds, one 1 KB fragment per instruction) into a
+// D-slot ring of KS k16 slices per step, and every wave reads its A and B fragments from
+// there. One workgroup per CU (BM = 384, KS = 4: 80 KB per slot, two slots = all 160 KB
+// of LDS; 8 waves of 192 accumulators). Accumulation order per output element is the
+// strip kernel's (k16 fragments in k order), so the two kernels give bitwise-equal results.
+template <int BM, int D, int NW, int KS>
+__global__ __launch_bounds__(64 * NW, 1) void tile2_gated_kernel(TileArgs a) {
+  constexpr int WMR = NW / 2;              // wave rows (2 wave columns)
+  constexpr int FM = BM / (32 * WMR);      // 32-row fragments per wave
+  constexpr int FN = 4;                    // 2 gate + 2 up 32-column tiles per wave
+  constexpr int TA = (BM / 32) * KS;       // A fragments per step (KS k16 slices deep)
+  constexpr int TB = 8 * KS;               // B fragments per step (8 tiles x KS k16)
+  constexpr int CPW = NW / KS;             // tiles covered by one copy index
+  constexpr int LA = TA / NW, LB = TB / NW;  // ... issued by each wave
+  constexpr int SLOT = (TA + TB) * 64;     // 16-byte LDS words per ring slot
+  constexpr int OUTC = 128, OP = OUTC + 8; // output columns, bf16 pitch of the parked tile
+  constexpr int PARK = (BM * OP * 2 + 15) / 16;
+  static_assert(BM % (32 * WMR) == 0 && TA % NW == 0 && TB % NW == 0 && D >= 2, "tile shape");
+  static_assert(NW % KS == 0 && 4 % CPW == 0, "copy assignment");
+  __shared__ bf16x8 lds[D * SLOT > PARK ? D * SLOT : PARK];
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  int id = blockIdx.x;
+  if (a.xcd_remap) id = (id & 7) * (gridDim.x >> 3) + (id >> 3);
+  const int mt = id % a.tiles_m, ntile = id / a.tiles_m;
+  const int m0 = mt * BM;
+  const int KT = a.K >> 4;
+  const int nsteps = a.ksteps;
+
+  const int arows = max(min(BM, a.M - m0), 0);
+  const __amdgpu_buffer_rsrc_t ar =
+      rows_rsrc_sgpr(a.a + (size_t)m0 * a.lda, arows * a.lda * (int)sizeof(__bf16));
+  // gate tiles ntile * 4 + c and up tiles likewise; one resource per weight, starting at
+  // this block's first tile (its 4 tiles are contiguous: [nt][kt] order)
+  const int wbytes = 4 * KT * 512 * (int)sizeof(__bf16);
+  const __amdgpu_buffer_rsrc_t gr = rows_rsrc_sgpr(a.w0 + (size_t)ntile * 4 * KT * 512, wbytes);
+  const __amdgpu_buffer_rsrc_t ur = rows_rsrc_sgpr(a.w1 + (size_t)ntile * 4 * KT * 512, wbytes);
+  // copy i of wave w is fragment q = i * NW + w of each operand (q = tile * KS + slice,
+  // slice w % KS, tile i * CPW + w / KS); the i-dependent parts of the offsets are
+  // wave-uniform (scalar), so each operand needs one lane offset
+  const int avoff = (((wave / KS) * 32 + (lane & 31)) * a.lda + (wave % KS) * 16 + (lane >> 5) * 8) *
+                    (int)sizeof(__bf16);
+  const int btile = KT * 512 * (int)sizeof(__bf16);
+  const int bvoff = ((wave % KS) * 512 + lane * 8) * (int)sizeof(__bf16) + (wave / KS) * btile;
+  const int arow_step = CPW * 32 * a.lda * (int)sizeof(__bf16);
+
+  auto issue = [&](int s, int slot) {
+    const int abase = s * KS * 16 * (int)sizeof(__bf16);
+    const int bbase = s * KS * 512 * (int)sizeof(__bf16);
+    bf16x8* dst = lds + slot * SLOT;
+#pragma unroll
+    for (int i = 0; i < LA; ++i)
+      buf_load16_lds_s(ar, &dst[(i * NW + wave) * 64], avoff, abase + i * arow_step);
+#pragma unroll
+    for (int i = 0; i < LB; ++i)     // tiles 0-3 gate, 4-7 up
+      buf_load16_lds_s(i * CPW < 4 ? gr : ur, &dst[(TA + i * NW + wave) * 64], bvoff,
+                       bbase + ((i * CPW) & 3) * btile);
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+#pragma unroll
+  for (int u = 0; u < D - 1; ++u) issue(u, u);
+
+  for (int s0 = 0; s0 < nsteps; s0 += D) {
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+      const int s = s0 + u;
+      // every copy of step s has landed (the D - 2 later steps may still be in flight)
+      __builtin_amdgcn_s_waitcnt(PI0_VMCNT((D - 2) * (LA + LB)));
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      // past the end a harmless re-load of the last step keeps the count per step fixed
+      issue(min(s + D - 1, nsteps - 1), (u + D - 1) % D);
+      __builtin_amdgcn_sched_barrier(0);
+      const bf16x8* st = lds + u * SLOT;
+#pragma unroll
+      for (int kq = 0; kq < KS; ++kq) {
+        bf16x8 bf[FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          const int tile = (j < 2 ? 0 : 4) + wn * 2 + (j & 1);
+          bf[j] = st[(TA + tile * KS + kq) * 64 + lane];
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const bf16x8 af = st[((wm * FM + i) * KS + kq) * 64 + lane];
+#pragma unroll
+          for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(af, bf[j], acc[i][j]);
+        }
+        __builtin_amdgcn_sched_barrier(0);   // bound the fragments held: 384 accumulators
+      }
+    }
+  }
+
+  // ---- epilogue: GeGLU in registers, parked as bf16 row-major, stored 16 bytes a lane
+  __builtin_amdgcn_s_waitcnt(PI0_VMCNT(0));
+  __syncthreads();
+  __bf16* cs = reinterpret_cast<__bf16*>(lds);
+  {
+    const int r = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = (wm * FM + i) * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          cs[row * OP + wn * 64 + j * 32 + r] = f2bf(gelu_tanh(acc[i][j][e]) * acc[i][2 + j][e]);
+      }
+  }
+  __syncthreads();
+  constexpr int C8 = OUTC / 8;
+  for (int idx = t; idx < BM * C8; idx += 64 * NW) {
+    const int row = idx / C8, c = (idx - row * C8) * 8;
+    const int grow = m0 + row, col = ntile * OUTC + c;
+    if (grow >= a.M || col >= a.n_valid) continue;
+    *reinterpret_cast<bf16x8*>(a.out + (size_t)grow * a.ldo + col) =
+        *reinterpret_cast<const bf16x8*>(&cs[row * OP + c]);
+  }
+}
+
 // W[batch][K][N] -> 32x32x16 B fragments: tile (nt, kt) of 16 k x 32 n is 64 lanes x 8 bf16,
 // lane = (k % 16 / 8) * 32 + n % 32, element k % 8; tiles ordered [nt][kt].
 // K_pad x N_pad (multiples of 16 / 32) with zeros outside the K x N source.
@@ -859,6 +995,24 @@ static int launch_tile_d4(TileArgs a, hipStream_t s) {
   return PI0HIP_ERR_SHAPE;
 }
 
+// Gated FFN on tile2_gated_kernel: BM-row x 128-output-column blocks, D-slot ring.
+template <int BM, int D, int NW, int KS>
+static int launch_tile2_gated(TileArgs a, hipStream_t s) {
+  const int kstep = KS * 16;
+  if (a.K % kstep || a.N % 128 || (a.K / kstep) % D) return PI0HIP_ERR_SHAPE;
+  if ((long long)a.K * 128 * (long long)sizeof(__bf16) > INT_MAX ||
+      (long long)BM * a.lda * (long long)sizeof(__bf16) > INT_MAX)
+    return PI0HIP_ERR_SHAPE;                 // 32-bit buffer offsets
+  a.tiles_m = (a.M + BM - 1) / BM;
+  a.tiles_n = a.N / 128;
+  a.splitk = 1;
+  a.ksteps = a.K / kstep;
+  const int grid = a.tiles_m * a.tiles_n;
+  a.xcd_remap = (grid % 8 == 0) ? 1 : 0;
+  hipLaunchKernelGGL((tile2_gated_kernel<BM, D, NW, KS>), dim3(grid), dim3(64 * NW), 0, s, a);
+  return (int)hipGetLastError();
+}
+
 static TileArgs tile_args(const void* x, int ldx, const void* w, void* out, int ldo, int M, int N,
                           int K) {
   TileArgs a = {};
@@ -956,6 +1110,13 @@ int pi0hip_tile_gated_ffn(const void* x, int ldx, const void* gate_packed, const
   if (misaligned(x, ldx) || misaligned(out, ldo)) return PI0HIP_ERR_SHAPE;
   TileArgs a = tile_args(x, ldx, gate_packed, out, ldo, M, N, K);
   a.w1 = (const __bf16*)up_packed;
+  // From 512 rows (the prefix encoder: 768, batched 3264) the 8-wave 384-row blocks with
+  // both operands in LDS (768 rows: 115 -> 103 us with cold weights, bitwise equal); below,
+  // where 384-row blocks would be mostly padding, the two-per-CU strip kernel.
+  if (M >= 512) {
+    const int e = launch_tile2_gated<384, 2, 8, 4>(a, s);
+    if (e != PI0HIP_ERR_SHAPE) return e;
+  }
   return launch_tile_auto<128, 64, 2, TE_GATE, true, 2>(a, s);
 }
 

@@ -160,6 +160,24 @@ def test_norm_gated_ffn(M):
     close(out, E.enc_norm_gated_ffn(x.float(), wg.float(), wu.float()), what=f"gated_ffn M={M}")
 
 
+def test_gated_ffn_row_blocks_bitwise():
+    """From 512 rows the gated FFN runs on 384-row 8-wave blocks with both operands in LDS,
+    below on the 128-row strip kernel; both accumulate every output in the same k order, so
+    the first 200 rows of an M = 768 (and of a ragged M = 600) product equal an M = 200
+    product bit for bit."""
+    x = rnd((768, 2048), 31, 1.0).to(DEV)
+    wg, wu = rnd((2048, 16384), 32, 0.02).to(DEV), rnd((2048, 16384), 33, 0.02).to(DEV)
+    outs = {}
+    for M in (768, 600, 200):
+        out = torch.zeros(M, 16384, dtype=torch.bfloat16, device=DEV)
+        xn = torch.zeros(M, 2048, dtype=torch.bfloat16, device=DEV)
+        EW.encoder_norm_gated_ffn(x[:M].contiguous(), wg, wu, out, xn)
+        outs[M] = out.cpu()
+    assert torch.equal(outs[768][:200], outs[200])
+    assert torch.equal(outs[600][:200], outs[200])
+    assert torch.equal(outs[768][:600], outs[600])
+
+
 def _encoder_case(layers, M, seed=40):
     from flash_vla_amd.weights import encoder_checkpoint, encoder_inputs
     ck = encoder_checkpoint(seed=seed, layers=layers)
