@@ -42,7 +42,7 @@ GATE_BYTES = 2 * 1024 * 4096 * 2           # gate + up weights of one layer (act
 # HBM bytes per launch from rocprofv3 FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (KiB; factors from a
 # plain 256 MiB copy); profiles/kernels_hbm_traffic_config2_config3.md
 GATE_TRAFFIC_BYTES = (8649.0 * 2.0 + 408.0 * 1.0) * 1024
-ENC_GATE_TRAFFIC_BYTES = (106977.4 * 2.0 + 24576.0 * 1.0) * 1024
+ENC_GATE_TRAFFIC_BYTES = (77975.5 * 2.0 + 24576.0 * 1.0) * 1024
 
 
 def _time_graph(run, n_inner, reps, torch):
@@ -181,7 +181,7 @@ def main_encoder(args, torch):
                 ck["encoder_ffn_up_w"][i % ENC_LAYERS], b["encoder_hidden"], b["encoder_x_norm"]),
                 n_inner=ENC_LAYERS, reps=10, torch=torch)
         achieved = gate_flops / (us * 1e-6) / 1e12
-        roof = {"kernel": "tile_gemm_kernel<TE_GATE> + rms_norm_kernel (encoder_norm_gated_ffn)",
+        roof = {"kernel": "tile2_gated_kernel + rms_norm_kernel (encoder_norm_gated_ffn)",
                 "bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
                 "traffic": int(ENC_GATE_TRAFFIC_BYTES), "avg_launch_us": round(us, 3), "flops_per_launch": gate_flops}
@@ -262,7 +262,7 @@ def main_full(args, torch):
                 n_inner=ENC_LAYERS, reps=10, torch=torch)
         gate_flops = 2 * M_enc * ENC_W * 2 * ENC_FFN
         achieved = gate_flops / (us * 1e-6) / 1e12
-        roof = {"kernel": "tile_gemm_kernel<TE_GATE> + rms_norm_kernel (encoder_norm_gated_ffn)",
+        roof = {"kernel": "tile2_gated_kernel + rms_norm_kernel (encoder_norm_gated_ffn)",
                 "bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
                 "traffic": int(ENC_GATE_TRAFFIC_BYTES) if not config5 else None,
