@@ -86,12 +86,34 @@ def kernel_roofline(eng, torch):
             "avg_launch_us": round(us, 3), "bytes_per_launch": GATE_BYTES}
 
 
+def host_threads() -> int:
+    """Threads for the CPU legs: the box's CPU share (OMP_NUM_THREADS, 16 on the GPU pool),
+    capped by the cores the OS reports."""
+    share = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
+    return max(1, min(os.cpu_count() or 1, share))
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def host_info(threads: int) -> dict:
+    return {"cores": threads, "host_cpus": os.cpu_count(), "cpu_model": cpu_model()}
+
+
 def cpu_baseline(seconds_budget: float = 20.0):
     import torch
     from oracle import pi0_decoder as O
     from flash_vla_amd.weights import decoder_checkpoint, decoder_inputs
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = host_threads()
     torch.set_num_threads(threads)
     ck = decoder_checkpoint(seed=0)
     inp = decoder_inputs(seed=1)
@@ -107,7 +129,7 @@ def cpu_baseline(seconds_budget: float = 20.0):
         if time.perf_counter() - t_start > 3 * seconds_budget:
             break
     return {"value": round(statistics.median(times), 2), "unit": "ms per 10-step chunk",
-            "cores": threads, "kind": "port",
+            **host_info(threads), "kind": "port",
             "sample": f"median of {len(times)} full 10-step chunks (fp32 PyTorch oracle, "
                       f"config 1 maths on the packed bf16 weights)"}
 
@@ -129,7 +151,7 @@ def encoder_flops(M=ENC_M, layers=ENC_LAYERS):
 def encoder_cpu_baseline(ck_cpu, x_cpu):
     import torch
     from oracle import pi0_encoder as E
-    threads = min(os.cpu_count() or 1, 16)
+    threads = host_threads()
     torch.set_num_threads(threads)
     one = {k: v[:2] for k, v in ck_cpu.items()}
     E.encoder_packed(one, x_cpu[:64], layers=2, bf16=False)          # warm the thread pool
@@ -140,7 +162,7 @@ def encoder_cpu_baseline(ck_cpu, x_cpu):
         t[n] = (time.perf_counter() - t0) * 1000.0
     full_layer = t[2] - t[1]
     est = (ENC_LAYERS - 1) * full_layer + t[1]
-    return {"value": round(est, 1), "unit": "ms per encode (M=768, 18 layers)", "cores": threads,
+    return {"value": round(est, 1), "unit": "ms per encode (M=768, 18 layers)", **host_info(threads),
             "kind": "port",
             "sample": f"fp32 PyTorch oracle timed on 1 full layer ({full_layer:.0f} ms) and the "
                       f"QKV-only last layer ({t[1]:.0f} ms) at M=768; value = 17 x full + last"}
@@ -303,7 +325,7 @@ def full_forward_cpu_baseline(batch: int, prompt: int):
     from oracle import pi0_encoder as E
     from oracle import pi0_vision as V
     from flash_vla_amd.weights import decoder_checkpoint, decoder_inputs, encoder_checkpoint
-    threads = min(os.cpu_count() or 1, 16)
+    threads = host_threads()
     torch.set_num_threads(threads)
     gen = torch.Generator().manual_seed(6)
     vw = {"vision_pre_attn_norm_w": torch.ones(1, 1152), "vision_pre_attn_norm_b": torch.zeros(1, 1152),
@@ -349,7 +371,7 @@ def full_forward_cpu_baseline(batch: int, prompt: int):
                      steps=STEPS, bf16=False)
     dec = (time.perf_counter() - t0) * 1000.0
     per_request = 27 * vis_layer + enc + dec
-    return {"value": round(batch * per_request, 1), "unit": "ms per full forward", "cores": threads,
+    return {"value": round(batch * per_request, 1), "unit": "ms per full forward", **host_info(threads),
             "kind": "port",
             "sample": f"fp32 PyTorch oracles, per request: 27 x one SigLIP layer ({vis_layer:.0f} ms), "
                       f"encoder at M={M} = 17 x one full layer ({t[2] - t[1]:.0f} ms) + the QKV-only "
@@ -413,22 +435,33 @@ def main():
     print(f"[bench] engine captured, {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
 
     stream = torch.cuda.current_stream()
-    for _ in range(args.warmup):
+    for _ in range(max(args.warmup, 3)):
         eng.buffers["diffusion_noise"].copy_(noise)
         eng.replay()
     torch.cuda.synchronize()
-    # timed region: exactly `steps` chunk replays (the noise is not reset in between;
-    # each replay is a full 10-step denoise of whatever the buffer holds)
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
+    # timed region: exactly `steps` chunk replays, each bracketed by its own pair of HIP
+    # events (the noise is not reset in between; each replay is a full 10-step denoise of
+    # whatever the buffer holds). value = the median replay; the mean over the whole
+    # bracket is reported beside it.
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    outer = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
     torch.cuda.synchronize()
-    start.record(stream)
-    for _ in range(args.steps):
+    outer[0].record(stream)
+    for s_ev, e_ev in evs:
+        s_ev.record(stream)
         eng.replay()
-    end.record(stream)
+        e_ev.record(stream)
+    outer[1].record(stream)
     torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
-    print(f"[bench] {ms:.3f} ms/chunk", file=sys.stderr, flush=True)
+    samples = sorted(s_ev.elapsed_time(e_ev) for s_ev, e_ev in evs)
+    ms = statistics.median(samples)
+    ms_mean = outer[0].elapsed_time(outer[1]) / args.steps
+    if args.steps < 30:
+        print(f"[bench] note: median of {args.steps} replays (>= 30 recommended)",
+              file=sys.stderr, flush=True)
+    print(f"[bench] {ms:.3f} ms/chunk (median of {args.steps}; bracket mean {ms_mean:.3f})",
+          file=sys.stderr, flush=True)
 
     roof = None if args.no_kernel else kernel_roofline(eng, torch)
     cpu = None if args.no_cpu else cpu_baseline()
@@ -448,6 +481,9 @@ def main():
         "hbm_gbs": round(gbs, 1),
         "loop_roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
         "bytes_per_chunk": CHUNK_BYTES,
+        "timing": {"statistic": f"median of {args.steps} individually timed replays",
+                   "ms_mean_bracket": round(ms_mean, 4), "ms_min": round(samples[0], 4),
+                   "ms_max": round(samples[-1], 4)},
         "roofline": roof,
         "cpu_baseline": cpu,
     }

@@ -32,7 +32,7 @@ constexpr int KP = ATT_HD + 8;      // bf16 pitch of staged K / Q rows
 constexpr int VP = ATT_HD + 16;     // bf16 pitch of staged V rows (544 B: 4 rows hit 4 bank groups)
 constexpr int OBP = ATT_HD + 4;     // fp32 pitch of the per-wave O buffer
 constexpr float NEG_BIG = -1.0e30f;
-constexpr int MAX_CHUNKS = 8;       // keys <= 1024
+constexpr int MAX_CHUNKS = 16;      // keys <= 2048 (prompts up to 1229 tokens with 3 views)
 constexpr int PF_MAX = 3;           // prefetch regions
 
 struct AttnArgs {

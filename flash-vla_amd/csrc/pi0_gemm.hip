@@ -20,6 +20,11 @@
 //   EPI_QKV_ROPE    f * x@W, RoPE, scatter     qkv + rope          (base.py:607-669)
 //   EPI_GATE        gelu(f x@Wg) * (f x@Wu)    gated FFN           (fused_norm.py:26-78)
 // with f = bf16(rsqrt(mean_k x^2 + 1e-6)) computed from the same A fragments.
+// The unfused call sites (op_table(fused=False)) take f from a prior rms-factor pass
+// and round x * f to bf16 per element before the MFMA, as the reference's two-kernel
+// path does:
+//   EPI_GATE_PRE         gelu(bf16(x f)@Wg) * (bf16(x f)@Wu)   (base.py:453-505)
+//   EPI_RMS_BIAS_RES_PRE out += b + bf16(x f)@W              (base.py:552-596)
 #include "pi0_common.h"
 #include "pi0_hip.h"
 
@@ -30,7 +35,8 @@ constexpr int MAX_SPLITK = 8;
 // 16 rows; one wave spreads the pass over 4x the CUs of a 64-row workgroup)
 constexpr int RED_THREADS = 64;
 
-enum Epi { EPI_BIAS = 0, EPI_RES = 1, EPI_RMS_BIAS_RES = 2, EPI_QKV_ROPE = 3, EPI_GATE = 4 };
+enum Epi { EPI_BIAS = 0, EPI_RES = 1, EPI_RMS_BIAS_RES = 2, EPI_QKV_ROPE = 3, EPI_GATE = 4,
+           EPI_GATE_PRE = 5, EPI_RMS_BIAS_RES_PRE = 6 };
 
 struct GemmArgs {
   const __bf16* x; int ldx;
@@ -44,12 +50,14 @@ struct GemmArgs {
   int M, N, K, splitk, heads, head_dim;
   int batch;              // EPI_QKV_ROPE: requests stacked "states first" (see gemm_epilogue)
   long long kv_bstride;   // EPI_QKV_ROPE: elements between two requests' K / V caches
-  float* out_f32;  // EPI_RMS_BIAS_RES: fp32 residual / destination instead of `out`
+  float* out_f32;  // EPI_RMS_BIAS_RES(_PRE): fp32 residual / destination instead of `out`
+  const __bf16* prescale;  // *_PRE: per-row bf16 factor applied to x before the MFMA
 };
 
 constexpr bool uses_rms(int epi) {
   return epi == EPI_RMS_BIAS_RES || epi == EPI_QKV_ROPE || epi == EPI_GATE;
 }
+constexpr bool uses_prescale(int epi) { return epi == EPI_GATE_PRE || epi == EPI_RMS_BIAS_RES_PRE; }
 
 // Per-tile scratch layout inside the workspace: [mb][nt][ks][64 rows][16 * ND] fp32,
 // then [mb][nt][ks][64] fp32 sums of squares. Counters live in a separate int array.
@@ -78,7 +86,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int row, int nt
     const __bf16* rp = a.out + (size_t)row * a.ldo + n;
 #pragma unroll
     for (int c = 0; c < 4; ++c) o[c] = v0[c] + bf2f(rp[c]);
-  } else if constexpr (EPI == EPI_RMS_BIAS_RES) {
+  } else if constexpr (EPI == EPI_RMS_BIAS_RES || EPI == EPI_RMS_BIAS_RES_PRE) {
     if (a.out_f32) {            // fp32 Euler accumulator: read, update and store in fp32
       float* rp = a.out_f32 + (size_t)row * a.ldo + n;
       const f32x4 r4 = *reinterpret_cast<const f32x4*>(rp);
@@ -91,7 +99,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int row, int nt
     const __bf16* rp = a.out + (size_t)row * a.ldo + n;
 #pragma unroll
     for (int c = 0; c < 4; ++c) o[c] = v0[c] * f + bf2f(a.bias[n + c]) + bf2f(rp[c]);
-  } else if constexpr (EPI == EPI_GATE) {
+  } else if constexpr (EPI == EPI_GATE || EPI == EPI_GATE_PRE) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) o[c] = gelu_tanh(v0[c] * f) * (v1[c] * f);
   } else if constexpr (EPI == EPI_QKV_ROPE) {
@@ -163,6 +171,14 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   auto swz = [](int row) { return BCH == 8 ? (row & 7) : ((row >> 1) & 3); };
   __bf16* xs = reinterpret_cast<__bf16*>(smem) + wave * 64 * KW;
   bf16x8 b0[KTW], b1[KTW];
+  // *_PRE: this lane's row factors (rows mt*16 + lane%16), loaded before the staging
+  // loads so that every k-block wait below also covers them
+  float fpre[4] = {1.f, 1.f, 1.f, 1.f};
+  if constexpr (uses_prescale(EPI)) {
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) fpre[mt] = bf2f(a.prescale[m0 + min(mt * 16 + (lane & 15), rows - 1)]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   PI0_PROBE(0);
   // ---- issue: this wave's x slice [64 x KW] goes straight from L2 into LDS (buffer
   // loads with the LDS destination), one k-block at a time, each followed by the
@@ -218,8 +234,12 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) {
       const int xrow = mt * 16 + r;
-      const bf16x8 av = *reinterpret_cast<const bf16x8*>(
+      bf16x8 av = *reinterpret_cast<const bf16x8*>(
           xs + (i / KB) * 64 * KB * 32 + xrow * KB * 32 + ((((i % KB) * 4 + g) ^ swz(xrow)) * 8));
+      if constexpr (uses_prescale(EPI)) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) av[j] = f2bf(bf2f(av[j]) * fpre[mt]);
+      }
       acc0[mt] = mfma16(av, b0[i], acc0[mt]);
       if constexpr (DUAL) acc1[mt] = mfma16(av, b1[i], acc1[mt]);
       if constexpr (RMS) {       // sum of squares with v_dot2 (two bf16 products per op)
@@ -523,6 +543,41 @@ int pi0hip_norm_qkv_rope(const void* x, int ldx, const void* wp, const void* rop
   }
   return pi0hip_norm_qkv_rope_batched(x, ldx, wp, rope, q, k, v, ldkv, 0, norm_factor, M, K, heads,
                                       head_dim, 1, s);
+}
+
+int pi0hip_scaled_gated_ffn(const void* x, int ldx, const void* f, const void* gate_p,
+                            const void* up_p, void* out, int ldo, int M, int N, int K,
+                            hipStream_t s) {
+  if (!x || !f || !gate_p || !up_p || !out) return PI0HIP_ERR_ARG;
+  GemmArgs a = base_args(x, ldx, gate_p, out, ldo, M, N, K, 1);
+  a.w1 = (const __bf16*)up_p;
+  a.prescale = (const __bf16*)f;
+  return launch_gemm<EPI_GATE_PRE, true>(a, s);
+}
+
+int pi0hip_scaled_linear_bias_residual(const void* x, int ldx, const void* f, const void* wp,
+                                       const void* bias, void* out, int ldo, int M, int N, int K,
+                                       int splitk, void* ws, size_t ws_bytes, hipStream_t s) {
+  if (!x || !f || !wp || !bias || !out) return PI0HIP_ERR_ARG;
+  GemmArgs a = base_args(x, ldx, wp, out, ldo, M, N, K, splitk);
+  a.bias = (const __bf16*)bias;
+  a.prescale = (const __bf16*)f;
+  if (int e = setup_ws(a, ws, ws_bytes, 0)) return e;
+  return launch_gemm<EPI_RMS_BIAS_RES_PRE, false>(a, s);
+}
+
+int pi0hip_scaled_linear_bias_residual_f32(const void* x, int ldx, const void* f, const void* wp,
+                                           const void* bias, float* out, int ldo, int M, int N,
+                                           int K, int splitk, void* ws, size_t ws_bytes,
+                                           hipStream_t s) {
+  if (!x || !f || !wp || !bias || !out) return PI0HIP_ERR_ARG;
+  if (ldo % 4) return PI0HIP_ERR_SHAPE;
+  GemmArgs a = base_args(x, ldx, wp, nullptr, ldo, M, N, K, splitk);
+  a.bias = (const __bf16*)bias;
+  a.out_f32 = out;
+  a.prescale = (const __bf16*)f;
+  if (int e = setup_ws(a, ws, ws_bytes, 0)) return e;
+  return launch_gemm<EPI_RMS_BIAS_RES_PRE, false>(a, s);
 }
 
 int pi0hip_norm_gated_ffn(const void* x, int ldx, const void* gate_p, const void* up_p,

@@ -1,37 +1,57 @@
-"""Graph-safe scratch memory (mirrors `src/flash_vla/runtime/cuda/arena.py:19-42`).
+"""Scratch buffers that survive hipGraph capture.
 
-Each (role, shape, dtype, device) buffer is allocated once, zeroed, and reused.
-After warmup the pool is frozen: a request that warmup did not cover raises
-instead of allocating inside a hipGraph capture.
+The interface (`get(role, shape, dtype, device)`, `freeze()`) is the one the
+reference's wrappers route scratch through (`src/flash_vla/runtime/cuda/arena.py:19-42`):
+a call site names a role and the shape it needs and gets the same device tensor
+back on every call. Buffers are created only while the pool is open (the warmup
+passes); `freeze()` closes it before capture, after which a request for a slot
+the warmup never created is a programming error -- it would put an allocation
+inside the graph -- and raises `LookupError`.
 """
 from __future__ import annotations
+
+from typing import NamedTuple
 
 import torch
 
 
+class _Slot(NamedTuple):
+    role: str
+    shape: tuple
+    dtype: torch.dtype
+    device: str
+
+
 class ScratchPool:
+    """Role-keyed, zero-initialised device scratch, open until `freeze()`."""
+
     def __init__(self) -> None:
-        self._buffers: dict = {}
-        self._frozen = False
+        self._slots: dict[_Slot, torch.Tensor] = {}
+        self._open = True
 
     def get(self, role: str, shape, dtype, device) -> torch.Tensor:
-        key = (role, tuple(shape), dtype, str(device))
-        buffer = self._buffers.get(key)
-        if buffer is None:
-            if self._frozen:
-                raise RuntimeError(
-                    f"ScratchPool is frozen but {key} was requested: warmup did not cover this "
-                    "shape, so it would allocate mid-capture.")
-            buffer = torch.zeros(shape, dtype=dtype, device=device)
-            self._buffers[key] = buffer
-        return buffer
+        slot = _Slot(role, tuple(int(d) for d in shape), dtype, str(device))
+        try:
+            return self._slots[slot]
+        except KeyError:
+            pass
+        if not self._open:
+            raise LookupError(
+                f"scratch slot {slot.role!r} {slot.shape} {slot.dtype} on {slot.device} was not "
+                "created during warmup; the pool is closed for graph capture")
+        tensor = torch.zeros(slot.shape, dtype=dtype, device=device)
+        self._slots[slot] = tensor
+        return tensor
 
     def freeze(self) -> None:
-        self._frozen = True
+        self._open = False
 
     @property
     def frozen(self) -> bool:
-        return self._frozen
+        return not self._open
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in self._slots.values())
 
     def __len__(self) -> int:
-        return len(self._buffers)
+        return len(self._slots)

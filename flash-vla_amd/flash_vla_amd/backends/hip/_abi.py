@@ -35,6 +35,15 @@ PROTOTYPES = {
     "pi0hip_attention_workspace_bytes": (c_size_t, [c_int, c_int]),
     "pi0hip_attention": (c_int, [P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int, c_int,
                                  c_int, P, c_size_t, P]),
+    # unfused decoder call sites
+    "pi0hip_rms_factor": (c_int, [P, c_int, P, c_int, c_int, P]),
+    "pi0hip_scaled_gated_ffn": (c_int, [P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, P]),
+    "pi0hip_scaled_linear_bias_residual": (c_int, [P, c_int, P, P, P, P, c_int, c_int, c_int,
+                                                   c_int, c_int, P, c_size_t, P]),
+    "pi0hip_scaled_linear_bias_residual_f32": (c_int, [P, c_int, P, P, P, P, c_int, c_int, c_int,
+                                                       c_int, c_int, P, c_size_t, P]),
+    "pi0hip_attention_unfused": (c_int, [P, c_int, P, P, c_int, P, c_int, P, c_int, P, c_int, c_int,
+                                         c_int, c_int, c_int, c_int, P]),
     # batched (config 5)
     "pi0hip_norm_qkv_rope_batched": (c_int, [P, c_int, P, P, P, P, P, c_int, ctypes.c_longlong, P,
                                              c_int, c_int, c_int, c_int, c_int, P]),

@@ -12,6 +12,7 @@ during warmup and frozen before capture.
 from __future__ import annotations
 
 import contextlib
+import weakref
 
 import torch
 
@@ -72,13 +73,36 @@ def _ptr(t: torch.Tensor):
 # and looked up by address on every later call.
 # ---------------------------------------------------------------------------
 class _PackedEntry:
-    __slots__ = ("src", "packed", "base", "nbytes", "K", "N", "version", "layout", "pad")
+    """Packed copy of one source weight. The tensor that owns the source's storage
+    (typically an engine's [L, K, N] stack) is held by weak reference: when it is freed,
+    the entry and its packed copy are dropped with it, so the cache never keeps a model
+    alive. The source itself (possibly a view, e.g. a reshape) is re-derived from the
+    owner when it is needed."""
+    __slots__ = ("owner_ref", "view", "packed", "base", "nbytes", "K", "N", "version", "layout",
+                 "pad", "__weakref__")
 
     def __init__(self, src, packed, K, N, layout, pad):
-        self.src, self.packed, self.K, self.N, self.layout, self.pad = src, packed, K, N, layout, pad
+        self.packed, self.K, self.N, self.layout, self.pad = packed, K, N, layout, pad
         self.base = src.data_ptr()
         self.nbytes = src.numel() * src.element_size()
         self.version = src._version
+        owner = src if src._base is None else src._base
+        self.view = (tuple(src.shape), tuple(src.stride()), src.storage_offset())
+        self.owner_ref = weakref.ref(owner, self._drop)
+
+    @property
+    def src(self):
+        owner = self.owner_ref()
+        if owner is None:
+            return None
+        shape, stride, offset = self.view
+        return owner.as_strided(shape, stride, offset)
+
+    def _drop(self, _ref) -> None:
+        try:
+            _PACKED.remove(self)
+        except ValueError:
+            pass
 
 
 _PACKED: list[_PackedEntry] = []
@@ -117,9 +141,12 @@ def packed_weight_ptr(w: torch.Tensor, layout: int = 16, pad: tuple | None = Non
     for e in _PACKED:
         if (e.K == K and e.N == N and e.layout == layout and e.pad == pad
                 and e.base <= ptr < e.base + e.nbytes):
-            if not _capturing() and e.version != e.src._version:
-                _pack_into(e.src, e.packed, K, N, layout, pad)
-                e.version = e.src._version
+            src = e.src
+            if src is None:
+                continue
+            if not _capturing() and e.version != src._version:
+                _pack_into(src, e.packed, K, N, layout, pad)
+                e.version = src._version
             return e.packed.data_ptr() + int((ptr - e.base) * scale)
     if _capturing():
         raise RuntimeError("weight was not packed before graph capture; run a warmup pass first")
@@ -158,6 +185,28 @@ def prepare_weights(weights: dict) -> None:
 
 def clear_packed_cache() -> None:
     _PACKED.clear()
+
+
+def packed_cache_bytes() -> int:
+    """Device bytes held by live packed copies."""
+    return sum(e.packed.numel() * e.packed.element_size() for e in _PACKED if e.src is not None)
+
+
+def repack_stale() -> int:
+    """Re-pack, in place, every packed copy whose source weight changed since it was packed
+    (outside graph capture). A captured graph reads the packed copies at fixed addresses,
+    so after updating an engine's weights in place this makes replays use the new values.
+    Returns the number of copies refreshed."""
+    if _capturing():
+        raise RuntimeError("repack_stale() cannot run during graph capture")
+    n = 0
+    for e in list(_PACKED):
+        src = e.src
+        if src is not None and src._version != e.version:
+            _pack_into(src, e.packed, e.K, e.N, e.layout, e.pad)
+            e.version = src._version
+            n += 1
+    return n
 
 
 def _splitk(M: int, N: int, K: int, target: int = 256) -> int:
@@ -399,6 +448,77 @@ def decoder_action_out_proj(x, weight, bias, out, norm_factor):
     return _action_out(x, weight, bias, out)
 
 
+# ---------------------------------------------------------------------------
+# Unfused call sites: op_table(fused=False) (the reference's wrappers.py:147-173, 192-208).
+# Same signatures; the reference's two-kernel rounding points.
+# ---------------------------------------------------------------------------
+def _rms_factor(x, norm_factor):
+    """norm_factor[:M] = bf16(rsqrt(mean(x^2) + 1e-6)) (wrappers.py:101-105)."""
+    _check(norm_factor, "norm_factor", 1)
+    M, K = x.shape
+    if norm_factor.shape[0] < M:
+        raise ValueError("norm_factor too short")
+    _abi.call("pi0hip_rms_factor", _ptr(x), x.stride(0), _ptr(norm_factor), M, K, _stream())
+    return norm_factor
+
+
+def decoder_norm_gated_ffn_unfused(x, gate_w, up_w, out, norm_factor):
+    """out = gelu(bf16(x*f) @ Wg) * (bf16(x*f) @ Wu), f written to norm_factor first
+    (wrappers.py:192-198 -> tl_rms_factor + tl_scaled_gate, base.py:453-505)."""
+    _check(x, "x", 2); _check(out, "out", 2)
+    M, K = x.shape
+    N = gate_w.shape[1]
+    if gate_w.shape != (K, N) or up_w.shape != (K, N) or out.shape != (M, N):
+        raise ValueError("decoder_norm_gated_ffn: shape mismatch")
+    _rms_factor(x, norm_factor)
+    _abi.call("pi0hip_scaled_gated_ffn", _ptr(x), x.stride(0), _ptr(norm_factor),
+              packed_weight_ptr(gate_w), packed_weight_ptr(up_w), _ptr(out), out.stride(0),
+              M, N, K, _stream())
+    return out
+
+
+def decoder_action_out_proj_unfused(x, weight, bias, out, norm_factor):
+    """Euler update out += bias + bf16(x*f) @ W, f written to norm_factor first
+    (wrappers.py:201-208 -> tl_rms_factor + tl_scaled_matmul_bias_res, base.py:552-596)."""
+    _check(x, "x", 2); _check(bias, "bias", 1); _check(out, "out", 2, allow_f32=True)
+    M, K = x.shape
+    N = weight.shape[1]
+    if weight.shape[0] != K or out.shape != (M, N) or bias.shape != (N,):
+        raise ValueError("decoder_action_out_proj: shape mismatch")
+    _rms_factor(x, norm_factor)
+    wp = packed_weight_ptr(weight)
+    s = _splitk(M, N, K)
+    ws, nbytes = _gemm_ws("gemm_ws_out", M, N, s, 0, x.device)
+    fn = ("pi0hip_scaled_linear_bias_residual_f32" if out.dtype == torch.float32
+          else "pi0hip_scaled_linear_bias_residual")
+    _abi.call(fn, _ptr(x), x.stride(0), _ptr(norm_factor), wp, _ptr(bias), _ptr(out),
+              out.stride(0), M, N, K, s, ws, nbytes, _stream())
+    return out
+
+
+def decoder_attention_unfused(Q, K, V, scores, out, encoder_seq_len):
+    """softmax_mask0(Q K^T * scale) @ V with the bf16 score matrix materialised in scratch
+    and the bf16 probabilities in `scores` ([rows, keys]); `out` may be `Q`
+    (wrappers.py:147-173). One request only, as in the reference."""
+    _check(Q, "Q", 2); _check(out, "out", 2)
+    if K.dim() != 2:
+        raise ValueError("the unfused decoder attention takes one request (K [keys, head_dim])")
+    _check(K, "K", 2); _check(V, "V", 2)
+    if scores is None:
+        raise ValueError("the unfused decoder attention needs the [rows, keys] scores buffer")
+    _check(scores, "scores", 2)
+    rows, head_dim = Q.shape
+    keys = K.shape[0]
+    if (V.shape != K.shape or K.shape[1] != head_dim or out.shape != Q.shape
+            or K.stride(0) != V.stride(0) or scores.shape[0] < rows or scores.shape[1] < keys):
+        raise ValueError("decoder_attention: shape mismatch")
+    raw = scratch("attn_scores", (rows, keys), torch.bfloat16, Q.device)
+    _abi.call("pi0hip_attention_unfused", _ptr(Q), Q.stride(0), _ptr(K), _ptr(V), K.stride(0),
+              _ptr(raw), raw.stride(0), _ptr(scores), scores.stride(0), _ptr(out), out.stride(0),
+              rows, keys, int(encoder_seq_len), DECODER_HEADS, head_dim, _stream())
+    return out
+
+
 DECODER_WRAPPERS = {
     "decoder_state_proj": decoder_state_proj,
     "decoder_action_in_proj": decoder_action_in_proj,
@@ -411,4 +531,11 @@ DECODER_WRAPPERS = {
     "decoder_action_out_proj": decoder_action_out_proj,
 }
 
+# op_table(fused=False): the unfused forms at the three call sites the reference's fused
+# overlay replaces (backends/tilelang/fused_wrappers.py:118-122)
 ALL_WRAPPERS = dict(DECODER_WRAPPERS)
+ALL_WRAPPERS.update({
+    "decoder_norm_gated_ffn": decoder_norm_gated_ffn_unfused,
+    "decoder_action_out_proj": decoder_action_out_proj_unfused,
+    "decoder_attention": decoder_attention_unfused,
+})

@@ -64,7 +64,9 @@ def allocate_decoder_buffers(encoder_seq_len: int, chunk_size: int, device,
         "decoder_state_buf": buf(B, width),
         "decoder_norm_factor_buf": buf(B * dec_len),
         "decoder_q_buf": buf(B * dec_len * heads, head_dim),
-        "decoder_attn_buf": buf(1, 1),      # unused by the fused attention (kept for the schema)
+        # probabilities of the unfused attention (op_table(fused=False), one request);
+        # the fused attention ignores it
+        "decoder_attn_buf": buf(dec_len * heads, cache_len) if B == 1 else buf(1, 1),
         "decoder_hidden": buf(B * dec_len, ffn),
     }
     buffers["decoder_rope_weights"].copy_(rope_table(dec_len, encoder_seq_len, head_dim, device))

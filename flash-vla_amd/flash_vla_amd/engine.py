@@ -31,6 +31,15 @@ def _attention_prefetch(backend, ops, enabled: bool):
     return pick(ops.decoder_attention) if enabled and pick is not None else None
 
 
+def _refresh(backend) -> int:
+    """Re-derive the backend's prepared (packed) weight copies from the engine's weights
+    after they were updated in place; the captured graph reads the copies at fixed
+    addresses, so its next replay uses the new values. Packed copies are not refreshed
+    during replay: weights are frozen between refreshes."""
+    fn = getattr(backend, "repack_stale", None)
+    return fn() if fn is not None else 0
+
+
 class Pi0DecoderEngine:
     """The captured 10-step decoder loop against a caller-supplied prefix KV cache.
 
@@ -128,6 +137,10 @@ class Pi0DecoderEngine:
         """Replay the captured loop on whatever the static buffers hold (benchmarks)."""
         self.graph.replay()
 
+    def refresh_weights(self) -> int:
+        """Call after updating `self.weights` in place (see `_refresh`)."""
+        return _refresh(self.backend)
+
 
 class Pi0EncoderEngine:
     """The captured prefix encoder: [M, 2048] input rows -> K/V cache rows of every layer."""
@@ -198,6 +211,10 @@ class Pi0EncoderEngine:
 
     def replay(self) -> None:
         self.graph.replay()
+
+    def refresh_weights(self) -> int:
+        """Call after updating `self.weights` in place (see `_refresh`)."""
+        return _refresh(self.backend)
 
 
 class Pi0Inference:
@@ -322,6 +339,10 @@ class Pi0Inference:
         else:
             self._run()
         return self.buffers["diffusion_noise"]
+
+    def refresh_weights(self) -> int:
+        """Call after updating `self.weights` in place (see `_refresh`)."""
+        return _refresh(self.backend)
 
 
 def _dims_from(weights: dict) -> dict:

@@ -147,12 +147,55 @@ int pi0hip_attention_prefetch(const void* q, int ldq, const void* k, const void*
 
 /* out = softmax(mask(q k^T / sqrt(head_dim))) v over `keys` cache rows; flat
  * query row r = token * heads + head; rows r < heads keep keys j <= enc_len.
- * `out` may alias `q`. head_dim must be 256, keys <= 1024.
+ * `out` may alias `q`. head_dim must be 256, keys <= 2048.
  * decoder_attention fused_wrappers.py:88-115 (tl_fd_flat_split + tl_fd_flat_combine,
  * kernels/base.py:801-923) */
 int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int ldkv, void* out,
                      int ldo, int rows, int keys, int enc_len, int heads, int head_dim,
                      void* ws, size_t ws_bytes, hipStream_t s);
+
+/* ---- unfused decoder call sites (op_table(fused=False)) ------------------------
+ * The reference's two-kernel decoder path, kept for its rounding points: the RMS
+ * factor is a separate pass that stores bf16 f, and x * f is rounded to bf16 per
+ * element before the GEMM; the attention materialises the bf16 score matrix and the
+ * bf16 probabilities. */
+
+/* f[m] = bf16(rsqrt(mean_k x[m, k]^2 + 1e-6)); K % 8 == 0, x 16-byte aligned.
+ * _rms_factor wrappers.py:101-105 (tl_rms_factor, kernels/base.py:344-370) */
+int pi0hip_rms_factor(const void* x, int ldx, void* f, int M, int K, hipStream_t s);
+
+/* out = bf16(gelu_tanh(a @ gate) * (a @ up)) with a = bf16(x * f[row]) per element;
+ * packed gate / up; same operand rules as pi0hip_norm_gated_ffn.
+ * decoder_norm_gated_ffn wrappers.py:192-198 (tl_scaled_gate, kernels/base.py:453-505) */
+int pi0hip_scaled_gated_ffn(const void* x, int ldx, const void* f, const void* gate_packed,
+                            const void* up_packed, void* out, int ldo, int M, int N, int K,
+                            hipStream_t s);
+
+/* out += bias + bf16(x * f[row]) @ w (bf16 out), split-K as pi0hip_linear_bias.
+ * decoder_action_out_proj wrappers.py:201-208 (tl_scaled_matmul_bias_res,
+ * kernels/base.py:552-596) */
+int pi0hip_scaled_linear_bias_residual(const void* x, int ldx, const void* f,
+                                       const void* w_packed, const void* bias, void* out, int ldo,
+                                       int M, int N, int K, int splitk, void* ws, size_t ws_bytes,
+                                       hipStream_t s);
+
+/* The same into an fp32 destination / residual (the fp32 Euler accumulator).
+ * Same reference call site. */
+int pi0hip_scaled_linear_bias_residual_f32(const void* x, int ldx, const void* f,
+                                           const void* w_packed, const void* bias, float* out,
+                                           int ldo, int M, int N, int K, int splitk, void* ws,
+                                           size_t ws_bytes, hipStream_t s);
+
+/* Three launches: scores = bf16((q k^T) / sqrt(head_dim)) [rows, keys];
+ * probs = bf16(softmax(mask(scores))) with masked keys filled with -3e38 (flat rows
+ * r < heads keep keys j <= enc_len); out = bf16(probs @ v). `out` may alias `q`;
+ * `scores` and `probs` must not alias. head_dim must be 256, keys <= 2048.
+ * decoder_attention wrappers.py:147-173 (tl_matmul_abT_scale, tl_softmax_mask0,
+ * tl_matmul: kernels/base.py:737-798, 84-111) */
+int pi0hip_attention_unfused(const void* q, int ldq, const void* k, const void* v, int ldkv,
+                             void* scores, int ld_scores, void* probs, int ld_probs, void* out,
+                             int ldo, int rows, int keys, int enc_len, int heads, int head_dim,
+                             hipStream_t s);
 
 /* ---- prefix encoder (M = 768..816 token rows, width 2048) --------------------
  * LDS-tiled MFMA GEMMs for the MFMA-bound encoder shapes (32x32x16 MFMAs);

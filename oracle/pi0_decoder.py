@@ -185,12 +185,54 @@ def op_action_out_proj(x, w, b, r, bf16=True):
 
 
 # ---------------------------------------------------------------------------
+# Unfused call sites (op_table(fused=False)): the same maths with the reference's
+# two-kernel rounding points
+# ---------------------------------------------------------------------------
+UNFUSED_MASK_NEG = -3.0e38     # tl_softmax_mask0's fill value (base.py:780)
+
+
+def op_attention_unfused(q, k, v, enc_len, heads, bf16=True):
+    """Unfused decoder attention (wrappers.py:147-173): S = bf16((q k^T) * hd^-0.5)
+    (tl_matmul_abT_scale, base.py:737-762); row softmax of the masked S in fp32 with a
+    finite fill, P = bf16(e / sum) (tl_softmax_mask0, base.py:765-798); out = bf16(P @ v)
+    (tl_matmul, base.py:84-111). Returns (out, P)."""
+    hd = q.shape[-1]
+    s = _bf((q @ k.t()) * (hd ** -0.5), bf16)
+    mask = attention_mask(q.shape[0], k.shape[0], enc_len, heads)
+    s = s.masked_fill(~mask, UNFUSED_MASK_NEG)
+    e = torch.exp(s - s.max(dim=-1, keepdim=True).values)
+    p = _bf(e / e.sum(dim=-1, keepdim=True), bf16)
+    return _bf(p @ v, bf16), p
+
+
+def op_norm_gated_ffn_unfused(x, wg, wu, bf16=True):
+    """Unfused gate (wrappers.py:192-198): f from tl_rms_factor (bf16), then
+    a = bf16(x * f) per element before the dual GEMM (tl_scaled_gate, base.py:496-497),
+    out = bf16(gelu(a @ Wg) * (a @ Wu)). Returns (out, f)."""
+    wt = x.dtype
+    f = rms_factor(x, bf16)
+    a = _bf(x * f[:, None], bf16)
+    return _bf(gelu_tanh(a @ wg.to(wt)) * (a @ wu.to(wt)), bf16), f
+
+
+def op_action_out_proj_unfused(x, w, b, r, bf16=True, round_out=True):
+    """Unfused Euler out-projection (wrappers.py:201-208): a = bf16(x * f) with the bf16
+    factor, out = r + b + a @ W in fp32 (tl_scaled_matmul_bias_res, base.py:552-596),
+    rounded when `round_out`."""
+    wt = r.dtype
+    f = rms_factor(x, bf16)[:, None]
+    a = _bf(x * f, bf16)
+    return _bf(r + b.to(wt) + a @ w.to(wt), round_out)
+
+
+# ---------------------------------------------------------------------------
 # Whole loops
 # ---------------------------------------------------------------------------
 def decoder_packed(weights: dict, state, noise, enc_k, enc_v, enc_len: int,
                    steps: int = 10, layers: int | None = None, bf16: bool = True,
                    dtype=torch.float32, heads: int = 8, trace: list | None = None,
-                   rope: torch.Tensor | None = None, fp32_noise: bool = False):
+                   rope: torch.Tensor | None = None, fp32_noise: bool = False,
+                   unfused: bool = False):
     """The packed decoder loop (pipeline.py:92-135) on CPU.
 
     `enc_k`/`enc_v` are the [layers, enc_len + T, hd] caches whose first
@@ -201,6 +243,7 @@ def decoder_packed(weights: dict, state, noise, enc_k, enc_v, enc_len: int,
     `rope` overrides the bf16 table of `rope_table` (an exact table is used by
     the fp64 folding identity).
     If `trace` is a list, per-step (noise, x) pairs are appended.
+    `unfused=True` runs the op_table(fused=False) call sites (the `*_unfused` ops).
     """
     w = {k: v.to(dtype) for k, v in weights.items()}
     n_layers = w["decoder_attn_qkv_w"].shape[0] if layers is None else layers
@@ -224,13 +267,28 @@ def decoder_packed(weights: dict, state, noise, enc_k, enc_v, enc_len: int,
             q, k, v, _ = op_norm_qkv_rope(x, w["decoder_attn_qkv_w"][i], rope, heads, bf16)
             K[i, enc_len:enc_len + T_] = k
             V[i, enc_len:enc_len + T_] = v
-            o = op_attention(q, K[i, :enc_len + T_], V[i, :enc_len + T_], enc_len, heads, bf16)
+            if unfused:
+                o, _ = op_attention_unfused(q, K[i, :enc_len + T_], V[i, :enc_len + T_],
+                                            enc_len, heads, bf16)
+            else:
+                o = op_attention(q, K[i, :enc_len + T_], V[i, :enc_len + T_], enc_len, heads,
+                                 bf16)
             x = op_matmul_residual(o.reshape(T_, -1), w["decoder_attn_o_w"][i], x, bf16)
-            hdn = op_norm_gated_ffn(x, w["decoder_ffn_gate_w"][i], w["decoder_ffn_up_w"][i], bf16)
+            if unfused:
+                hdn, _ = op_norm_gated_ffn_unfused(x, w["decoder_ffn_gate_w"][i],
+                                                   w["decoder_ffn_up_w"][i], bf16)
+            else:
+                hdn = op_norm_gated_ffn(x, w["decoder_ffn_gate_w"][i], w["decoder_ffn_up_w"][i],
+                                        bf16)
             x = op_matmul_residual(hdn, w["decoder_ffn_down_w"][i], x, bf16)
-        noise = op_action_out_proj(x[1:], w["decoder_action_fused_out_proj_w"],
-                                   w["decoder_action_fused_out_proj_b"], noise,
-                                   bf16 and not fp32_noise)
+        if unfused:
+            noise = op_action_out_proj_unfused(x[1:], w["decoder_action_fused_out_proj_w"],
+                                               w["decoder_action_fused_out_proj_b"], noise,
+                                               bf16, bf16 and not fp32_noise)
+        else:
+            noise = op_action_out_proj(x[1:], w["decoder_action_fused_out_proj_w"],
+                                       w["decoder_action_fused_out_proj_b"], noise,
+                                       bf16 and not fp32_noise)
         if trace is not None:
             trace.append((noise.clone(), x.clone()))
     return noise, x, K, V

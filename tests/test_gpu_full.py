@@ -145,12 +145,12 @@ def test_ffn_down_ragged_k():
     close(out.reshape(768, 1152), ref.bfloat16().float(), what="vision ffn_down")
 
 
-def _shallow_checkpoint(seed=90, vis=2, enc=2, dec=2):
+def _shallow_checkpoint(seed=90, vis=2, enc=2, dec=2, prompt_len=0):
     """random_checkpoint()'s tensors (N(0,1) x 0.05, schema order) with short layer stacks."""
     from flash_vla_amd.spec import weight_shapes
     g = torch.Generator().manual_seed(seed)
     out = {}
-    for name, shape in weight_shapes(0).items():
+    for name, shape in weight_shapes(prompt_len).items():
         if name.startswith(("vision_attn", "vision_ffn", "vision_pre")):
             shape = (vis,) + tuple(shape[1:])
         elif name.startswith(("encoder_attn", "encoder_ffn")):
@@ -190,6 +190,29 @@ def test_full_forward_shallow(full_case):
               f"bf16 oracle err {e_err:.3e} 1-cos {1 - e_cos:.2e}", flush=True)
         assert g_cos >= 0.999
         assert (1 - g_cos) <= 1.5 * (1 - e_cos) + 1e-6 and g_err <= 1.5 * e_err + 2e-3
+
+
+def test_full_forward_default_prompt_256():
+    """random_checkpoint()'s default prompt_len=256 (weights.py:10 of the reference): prefix
+    1024 tokens, decoder keys 1075 (9 key chunks), 1 layer each, 1 Euler step."""
+    from flash_vla_amd import Pi0Inference
+    ck = _shallow_checkpoint(seed=95, vis=1, enc=1, dec=1, prompt_len=256)
+    g = torch.Generator().manual_seed(96)
+    images = (torch.rand(3, 224, 224, 3, generator=g) * 2 - 1).to(torch.bfloat16)
+    state = torch.randn(32, generator=g).to(torch.bfloat16)
+    noise = torch.randn(50, 32, generator=g).to(torch.bfloat16)
+    eng = Pi0Inference({k: v.to(DEV) for k, v in ck.items()}, num_views=3, chunk_size=50,
+                       steps=1)
+    assert eng.encoder_seq_len == 1024 and eng.buffers["encoder_K"].shape[1] == 1075
+    out = eng.forward(images.to(DEV), state.to(DEV), noise.to(DEV)).clone()
+    bn, _, _ = Vn.full_forward(ck, images, state, noise, steps=1, bf16=True)
+    fn, _, _ = Vn.full_forward(ck, images, state, noise, steps=1, bf16=False)
+    g_err, g_cos = metrics(out, fn)
+    e_err, e_cos = metrics(bn, fn)
+    print(f"prompt 256 forward: gpu vs fp32 err {g_err:.3e} 1-cos {1 - g_cos:.2e}; "
+          f"bf16 oracle err {e_err:.3e} 1-cos {1 - e_cos:.2e}", flush=True)
+    assert g_cos >= 0.999
+    assert (1 - g_cos) <= 1.5 * (1 - e_cos) + 1e-6 and g_err <= 1.5 * e_err + 2e-3
 
 
 def test_full_forward_graph_equals_eager(full_case):

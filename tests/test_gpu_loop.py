@@ -155,3 +155,78 @@ def test_prefetch_does_not_change_the_chunk(case):
         outs.append(eng.forward(inp["observation_state_normalized"].to(DEV),
                                 inp["diffusion_noise"].to(DEV)).clone())
     assert torch.equal(outs[0], outs[1])
+
+
+def _p99(got, ref):
+    d = (got.float().cpu() - ref.float().cpu()).abs().flatten()
+    return d.kthvalue(max(1, int(0.99 * d.numel()))).values.item()
+
+
+@pytest.mark.parametrize("steps", [1, 10])
+def test_reference_contract_vs_bf16_oracle(case, steps):
+    """`fp32_euler=False` keeps the reference's contract: `diffusion_noise` is bf16 and is
+    re-rounded every Euler step (pipeline.py:105,132). Compared with the oracle that rounds
+    at the same points (`bf16=True`, bf16 noise), the two differ only in fp32 summation
+    order. Criterion: after 1 step max abs <= 2e-2 and cosine >= 0.99999. After 10 steps,
+    where the chunk is re-rounded ten times and rounding differences compound through the
+    chaotic loop: max abs <= 2 bf16 ulps and p99 <= 1 ulp at the chunk's largest magnitude,
+    cosine >= 0.9999, and the GPU's mean distance from the fp32 oracle at most 1.25x that
+    of exact bf16 emulation (two bf16 implementations of the loop sit about as far from
+    each other as either sits from fp32)."""
+    eng = _engine(case, steps, 18, capture=True, fp32_euler=False)
+    out = eng.forward(case[1]["observation_state_normalized"].to(DEV),
+                      case[1]["diffusion_noise"].to(DEV)).clone()
+    emu = _oracle(case, steps, 18, bf16=True)[0]
+    f32 = _oracle(case, steps, 18, bf16=False)[0]
+    err, cos = _metrics(out, emu)
+    e_err, _ = _metrics(emu, f32)
+    print(f"\nreference contract, {steps} step(s): vs bf16 oracle max abs {err:.3e} "
+          f"p99 {_p99(out, emu):.3e} cos {cos:.7f}; bf16 oracle vs fp32 max abs {e_err:.3e}")
+    if steps == 1:
+        assert err <= 2e-2 and cos >= 0.99999
+    else:
+        import math
+        ulp = 2.0 ** (math.floor(math.log2(emu.abs().max().item())) - 7)
+        mean = (out.float().cpu() - emu).abs().mean().item()
+        g_mean = (out.float().cpu() - f32).abs().mean().item()
+        e_mean = (emu - f32).abs().mean().item()
+        print(f"bf16 ulp {ulp:.4f}; mean abs vs bf16 oracle {mean:.2e}; vs fp32: gpu "
+              f"{g_mean:.2e}, bf16 oracle {e_mean:.2e}")
+        assert err <= 2 * ulp and _p99(out, emu) <= ulp and cos >= 0.9999
+        assert g_mean <= 1.25 * e_mean
+
+
+def test_engines_release_their_weights(case):
+    """Two engines built and dropped in one process: the packed-weight cache holds its
+    sources weakly, so device memory returns to where it started."""
+    import gc
+    from flash_vla_amd.backends.hip import wrappers as Wr
+    gc.collect()
+    torch.cuda.synchronize()
+    base_mem, base_cache = torch.cuda.memory_allocated(), Wr.packed_cache_bytes()
+    for _ in range(2):
+        eng = _engine(case, 1, 2, capture=True)
+        assert Wr.packed_cache_bytes() > base_cache
+        del eng
+        gc.collect()
+        torch.cuda.synchronize()
+        assert Wr.packed_cache_bytes() == base_cache
+    assert torch.cuda.memory_allocated() <= base_mem + (1 << 20)
+
+
+def test_refresh_weights_reaches_the_graph(case):
+    """Weights updated in place after capture reach the replayed graph once
+    `refresh_weights()` has re-packed them."""
+    ck, inp = case
+    state = inp["observation_state_normalized"].to(DEV)
+    noise0 = inp["diffusion_noise"].to(DEV)
+    eng = _engine(case, 1, 2, capture=True)
+    before = eng.forward(state, noise0).clone()
+    eng.weights["decoder_ffn_gate_w"].mul_(-1.0)
+    assert eng.refresh_weights() >= 1
+    after = eng.forward(state, noise0).clone()
+    flipped = dict(ck)
+    flipped["decoder_ffn_gate_w"] = -ck["decoder_ffn_gate_w"]
+    fresh = _engine((flipped, inp), 1, 2, capture=True)
+    assert not torch.equal(before, after)
+    assert torch.equal(after, fresh.forward(state, noise0))

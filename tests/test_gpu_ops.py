@@ -111,7 +111,8 @@ def test_norm_qkv_rope(M):
 
 
 @pytest.mark.parametrize("rows,keys,enc", [(408, 819, 768), (408, 867, 816), (16, 64, 40),
-                                           (24, 100, 60), (8, 769, 768), (1632, 819, 768)])
+                                           (24, 100, 60), (8, 769, 768), (1632, 819, 768),
+                                           (408, 1024, 973), (408, 1075, 1024), (408, 2048, 1997)])
 def test_attention_matches_masked_softmax(rows, keys, enc):
     q = rnd((rows, 256), 13)
     k = rnd((keys, 256), 14)
@@ -121,6 +122,12 @@ def test_attention_matches_masked_softmax(rows, keys, enc):
     W.decoder_attention(Q, k.to(DEV), v.to(DEV), scores, Q, enc)   # out aliases Q
     ref = O.op_attention(q.float(), k.float(), v.float(), enc, 8)
     close(Q, ref, tol=2.0 ** -5, what="attention")
+
+
+def test_attention_rejects_more_than_2048_keys():
+    q, k = rnd((16, 256), 13).to(DEV), rnd((2049, 256), 14).to(DEV)
+    with pytest.raises(RuntimeError):
+        W.decoder_attention(q, k, k, None, q, 1998)
 
 
 def test_attention_state_rows_ignore_action_keys():

@@ -107,8 +107,9 @@ def test_scratch_pool_freeze():
     assert pool.get("r", (4,), torch.float32, "cpu") is a
     pool.freeze()
     assert pool.get("r", (4,), torch.float32, "cpu") is a
-    with pytest.raises(RuntimeError):
+    with pytest.raises(LookupError):
         pool.get("r", (5,), torch.float32, "cpu")
+    assert len(pool) == 1 and pool.nbytes() == 16 and pool.frozen
 
 
 def test_splitk_choice_fills_the_chip():

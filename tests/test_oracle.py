@@ -291,3 +291,79 @@ def test_bf16_mode_close_to_fp32_small():
     b, _, _, _ = O.decoder_packed(packed, state, noise, K, V, enc_len, steps=2, bf16=False,
                                   heads=SMALL["heads"])
     assert (a - b).abs().max() < 3e-2
+
+
+# ---------------------------------------------------------------------------
+# Unfused call sites (op_table(fused=False))
+# ---------------------------------------------------------------------------
+def test_unfused_loop_equals_fused_without_rounding_fp64():
+    """Without bf16 rounding the unfused and fused plans are the same function: the whole
+    unfolded-vs-packed identity above then pins the unfused ops too (a dropped factor, a
+    wrong mask fill or a transposed operand breaks the equality)."""
+    layers, enc_len, chunk = 2, 20, 5
+    p, state, noise, pk, pv = _small_case(layers, enc_len, chunk)
+    packed = W.fold_decoder(p, out_dtype=torch.float64)
+    T_ = chunk + 1
+    K = torch.cat([pk, torch.zeros(layers, T_, pk.shape[-1], dtype=torch.float64)], 1)
+    V = torch.cat([pv, torch.zeros(layers, T_, pv.shape[-1], dtype=torch.float64)], 1)
+    kw = dict(steps=3, bf16=False, dtype=torch.float64, heads=SMALL["heads"])
+    a = O.decoder_packed(packed, state, noise, K, V, enc_len, unfused=False, **kw)[0]
+    b = O.decoder_packed(packed, state, noise, K, V, enc_len, unfused=True, **kw)[0]
+    assert torch.allclose(a, b, atol=1e-11, rtol=1e-11)
+
+
+def test_unfused_attention_brute_force_fp64():
+    """Unfused attention without rounding == per-row loops with explicit mask; with
+    rounding, P rows sum to 1 within bf16 rounding and masked keys get exactly 0."""
+    g = torch.Generator().manual_seed(71)
+    heads, T_, enc, hd = 2, 3, 5, 8
+    q = torch.randn(T_ * heads, hd, generator=g, dtype=torch.float64)
+    k = torch.randn(enc + T_, hd, generator=g, dtype=torch.float64)
+    v = torch.randn(enc + T_, hd, generator=g, dtype=torch.float64)
+    out, _ = O.op_attention_unfused(q, k, v, enc, heads, bf16=False)
+    for r in range(q.shape[0]):
+        keys = [j for j in range(k.shape[0]) if r >= heads or j <= enc]
+        s = [sum(q[r, d] * k[j, d] for d in range(hd)) / math.sqrt(hd) for j in keys]
+        m = max(s)
+        e = [math.exp(x - m) for x in s]
+        z = sum(e)
+        ref = [sum(e[i] / z * v[j, d] for i, j in enumerate(keys)) for d in range(hd)]
+        assert torch.allclose(out[r], torch.tensor(ref, dtype=torch.float64), atol=1e-12)
+    _, p = O.op_attention_unfused(q.float(), k.float(), v.float(), enc, heads, bf16=True)
+    assert torch.all(p[:heads, enc + 1:] == 0)
+    assert torch.allclose(p.sum(-1), torch.ones(p.shape[0]), atol=2e-2)
+
+
+def test_unfused_rounding_points_known_answers():
+    """Hand-worked values of the unfused rounding points.
+
+    Gate / out-proj: x = 1 + 2^-7 in every column of a 256-wide row gives
+    f = bf16(1/sqrt(1.0156..+1e-6)) = 0.9921875 and x*f = 0.99993896484375, which bf16 rounds
+    to 1.0. With W = e_0 the unfused gate is bf16(gelu(1) * 1); with W = all ones and an fp32
+    destination the unfused out-projection is exactly 256 while the fused one (factor on the
+    fp32 accumulator) is 0.9921875 * 258 = 255.984375.
+    Scores: q.k = 1.00390625 (1 + 2^-8) with hd = 1 is not a bf16 value and rounds to 1.0 (ties
+    to even) before the softmax."""
+    K = 256
+    x = torch.full((1, K), 1.0 + 2.0 ** -7)
+    f = O.rms_factor(x, True)
+    assert f.item() == 0.9921875
+    wg = torch.zeros(K, 1)
+    wg[0, 0] = 1.0
+    wu = wg.clone()
+    out, _ = O.op_norm_gated_ffn_unfused(x, wg, wu, bf16=True)
+    assert out.item() == O._bf(O.gelu_tanh(torch.tensor(1.0)) * 1.0, True).item()
+    r = torch.zeros(1, 1)
+    b = torch.zeros(1)
+    ones = torch.ones(K, 1)
+    assert O.op_action_out_proj_unfused(x, ones, b, r, bf16=True, round_out=False).item() == 256.0
+    fused_fp32 = (x @ ones) * f                       # the fused form's fp32 value
+    assert fused_fp32.item() == 255.984375
+    q = torch.tensor([[1.0]])
+    kk = torch.tensor([[1.00390625], [0.0]])
+    vv = torch.tensor([[2.0], [0.0]])
+    o, p = O.op_attention_unfused(q, kk, vv, enc_len=1, heads=1, bf16=True)
+    # S = [1.0, 0.0] after rounding: p = [e/(e+1), 1/(e+1)] rounded to bf16
+    e = math.exp(1.0)
+    assert p[0, 0].item() == O._bf(torch.tensor(e / (e + 1.0)), True).item()
+    assert p[0, 1].item() == O._bf(torch.tensor(1.0 / (e + 1.0)), True).item()
