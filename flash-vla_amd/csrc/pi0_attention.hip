@@ -33,7 +33,7 @@ constexpr int VP = ATT_HD + 16;     // bf16 pitch of staged V rows (544 B: 4 row
 constexpr int OBP = ATT_HD + 4;     // fp32 pitch of the per-wave O buffer
 constexpr float NEG_BIG = -1.0e30f;
 constexpr int MAX_CHUNKS = 16;      // keys <= 2048 (prompts up to 1229 tokens with 3 views)
-constexpr int PF_MAX = 3;           // prefetch regions
+constexpr int PF_MAX = 4;           // prefetch regions
 
 struct AttnArgs {
   const __bf16* q; int ldq;
@@ -69,7 +69,7 @@ __device__ __forceinline__ void prefetch_slices(const AttnArgs& a) {
     const int lines = a.pf_slice_words[r] / 32;
     const int items = (a.pf_nslices[r] - x + 7) / 8 * lines;
     const unsigned* base = a.pf_base[r];
-    for (int it = j * 256 + t; it < items; it += per_xcd * 256) {
+    for (int it = j * (int)blockDim.x + t; it < items; it += per_xcd * (int)blockDim.x) {
       const int sl = x + 8 * (it / lines), l = it - (it / lines) * lines;
       acc += base[(size_t)sl * a.pf_slice_words[r] + l * 32];
     }
@@ -87,7 +87,46 @@ __device__ __forceinline__ int out_row(const AttnArgs& a, int b, int lr) {
   return tok * a.heads + head;
 }
 
-__global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
+// Merge of one 16-byte output piece (row, columns col..col+3) over the key chunks, in chunk
+// order: O = sum_c 2^(lse_c - max) O_c / sum_c 2^(lse_c - max).
+__device__ __forceinline__ bf16x4 merge_piece(__amdgpu_buffer_rsrc_t pr, __amdgpu_buffer_rsrc_t lr,
+                                              int nchunks, int rows_pad, int row, int col) {
+  float lse_c[MAX_CHUNKS];
+  f32x4 pv[MAX_CHUNKS];
+#pragma unroll
+  for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
+    const int ci = min(cc, nchunks - 1);
+    lse_c[cc] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                              lr, (ci * rows_pad + row) * 4, 0, 0));
+    pv[cc] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           pr, ((ci * rows_pad + row) * ATT_HD + col) * 4, 0, 0));
+  }
+  float lmax = NEG_BIG;
+#pragma unroll
+  for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
+    lse_c[cc] = cc < nchunks ? lse_c[cc] : NEG_BIG;
+    lmax = fmaxf(lmax, lse_c[cc]);
+  }
+  float wsum = 0.f;
+  f32x4 o4 = zero4();
+#pragma unroll
+  for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
+    const float w = cc < nchunks ? fast_exp2(lse_c[cc] - lmax) : 0.f;
+    wsum += w;
+    o4 += w * pv[cc];
+  }
+  const float winv = wsum > 0.f ? __builtin_amdgcn_rcpf(wsum) : 0.f;
+  return bf16x4{f2bf(o4[0] * winv), f2bf(o4[1] * winv), f2bf(o4[2] * winv), f2bf(o4[3] * winv)};
+}
+
+// NWV waves: 4 key groups of 32 keys x NWV / 4 slices of the head dimension for P @ V
+// (with 8 waves each S is computed twice, and every wave issues half the staging loads).
+template <int NWV>
+__global__ __launch_bounds__(NWV * 64, 2) void attn_kernel(AttnArgs a) {
+  constexpr int NT = NWV * 64;              // threads
+  constexpr int RP = NT / 32;               // staged rows per pass (32 16-byte chunks per row)
+  constexpr int KPASS = ATT_CH / RP, QPASS = ATT_QT / RP > 0 ? ATT_QT / RP : 1;
+  constexpr int NDH = NWV / 4, DTW = 16 / NDH;   // head-dim slices, 16-column tiles per wave
   // One LDS area holds K (pitch KP) for S, then V (pitch VP) for P @ V, then the fp32
   // per-wave O buffer: ~79 KB in all, so two workgroups fit on a CU (batched requests).
   __shared__ __attribute__((aligned(16))) __bf16 kv_[ATT_CH * VP];
@@ -103,6 +142,7 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   }
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int r = lane & 15, g = lane >> 4;
+  const int kg = wave & 3, dh = wave >> 2;  // key group, head-dim slice
   const int qt = blockIdx.x % a.nqt, c = blockIdx.x / a.nqt;
   const int q0 = qt * ATT_QT, k0 = c * ATT_CH;
   const int bq = blockIdx.y;
@@ -116,8 +156,8 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   // ---- stage K, V, Q with coalesced loads. The buffer resources end at the last
   // key / query row: rows past the end load as zeros (such keys are masked out
   // below, such query rows are never stored).
-  bf16x8 vv[16];
-  const int row0 = t >> 5, ch = t & 31;                    // 8 rows x 32 chunks per pass
+  bf16x8 vv[KPASS];
+  const int row0 = t >> 5, ch = t & 31;                    // RP rows x 32 chunks per pass
   {
     const int kbytes = max(a.keys - k0, 0) * a.ldkv * (int)sizeof(__bf16);
     const __amdgpu_buffer_rsrc_t kr = rows_rsrc(a.k + (size_t)k0 * a.ldkv, kbytes);
@@ -125,28 +165,28 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
     const __amdgpu_buffer_rsrc_t qr =
         rows_rsrc(a.q + (size_t)q0 * a.ldq, max(a.rows - q0, 0) * a.ldq * (int)sizeof(__bf16));
     const int koff = (row0 * a.ldkv + ch * 8) * (int)sizeof(__bf16);
-    const int kstep = 8 * a.ldkv * (int)sizeof(__bf16);
+    const int kstep = RP * a.ldkv * (int)sizeof(__bf16);
     const int qoff = (row0 * a.ldq + ch * 8) * (int)sizeof(__bf16);
-    const int qstep = 8 * a.ldq * (int)sizeof(__bf16);
-    bf16x8 kv[16], qv[2];
+    const int qstep = RP * a.ldq * (int)sizeof(__bf16);
+    bf16x8 kv[KPASS], qv[QPASS];
     // issue order = order of use: Q, K, then V (loads return in order). Q and K are
     // published first; V lands while S = K Q^T and the softmax run.
 #pragma unroll
-    for (int j = 0; j < 2; ++j) qv[j] = buf_load8(qr, qoff + j * qstep);
+    for (int j = 0; j < QPASS; ++j) qv[j] = buf_load8(qr, qoff + j * qstep);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) kv[j] = buf_load8(kr, koff + j * kstep);
+    for (int j = 0; j < KPASS; ++j) kv[j] = buf_load8(kr, koff + j * kstep);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) vv[j] = buf_load8(vr, koff + j * kstep);
+    for (int j = 0; j < KPASS; ++j) vv[j] = buf_load8(vr, koff + j * kstep);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) *reinterpret_cast<bf16x8*>(&qs_[row0 + 8 * j][ch * 8]) = qv[j];
+    for (int j = 0; j < QPASS; ++j) *reinterpret_cast<bf16x8*>(&qs_[row0 + RP * j][ch * 8]) = qv[j];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) *reinterpret_cast<bf16x8*>(&ks_[row0 + 8 * j][ch * 8]) = kv[j];
+    for (int j = 0; j < KPASS; ++j) *reinterpret_cast<bf16x8*>(&ks_[row0 + RP * j][ch * 8]) = kv[j];
   }
   __syncthreads();
   PI0_PROBE(1);
 
   // ---- S^T tiles of this wave: lane holds query row q0+r, keys kw + nt*16 + 4g + i
-  const int kw = wave * 32;
+  const int kw = kg * 32;
   f32x4 st[2] = {zero4(), zero4()};
 #pragma unroll
   for (int ks = 0; ks < 8; ++ks) {
@@ -185,12 +225,12 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   }
   lsum += __shfl_xor(lsum, 16, PI0_WAVE);
   lsum += __shfl_xor(lsum, 32, PI0_WAVE);
-  if (g == 0) { sm[wave][r] = mx; sl[wave][r] = lsum; }
+  if (g == 0 && dh == 0) { sm[kg][r] = mx; sl[kg][r] = lsum; }
 
   __syncthreads();          // every wave is done reading K: V takes its place
   // ---- publish V (its loads were in flight during S and the softmax)
 #pragma unroll
-  for (int j = 0; j < 16; ++j) *reinterpret_cast<bf16x8*>(&vs_[row0 + 8 * j][ch * 8]) = vv[j];
+  for (int j = 0; j < KPASS; ++j) *reinterpret_cast<bf16x8*>(&vs_[row0 + RP * j][ch * 8]) = vv[j];
   __syncthreads();
   PI0_PROBE(2);
   // ---- O_w = P V_w : B fragment = V[keys kw + {4g..4g+3, 16+4g..16+4g+3}][column].
@@ -198,11 +238,11 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   // k receives element j % 4 of the 8 bytes at lane 4k + j / 4's address, so lane
   // 4k + c points at V[kw + 4g + k][16 dt + 4c .. +3] and lane r (column 16 dt + r)
   // gets keys 4g .. 4g + 3 of its column.
-  f32x4 o[16];
+  f32x4 o[DTW];
   typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-  const int vkey = kw + 4 * g + (r >> 2), vcol = (r & 3) * 4;
+  const int vkey = kw + 4 * g + (r >> 2), vcol = dh * DTW * 16 + (r & 3) * 4;
 #pragma unroll
-  for (int dt = 0; dt < 16; ++dt) {
+  for (int dt = 0; dt < DTW; ++dt) {
     const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
         (lds_bf16x4*)&vs_[vkey][dt * 16 + vcol]);
     const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
@@ -221,14 +261,14 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
     float M = NEG_BIG;
 #pragma unroll
     for (int w = 0; w < 4; ++w) M = fmaxf(M, sm[w][qr]);
-    alpha[i] = fast_exp2(sm[wave][qr] - M);   // 0 for an empty wave next to a non-empty one
+    alpha[i] = fast_exp2(sm[kg][qr] - M);     // 0 for an empty wave next to a non-empty one
   }
   float* ob = reinterpret_cast<float*>(kv_);             // [4][16][OBP] fp32
 #pragma unroll
-  for (int dt = 0; dt < 16; ++dt)
+  for (int dt = 0; dt < DTW; ++dt)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      ob[(wave * ATT_QT + g * 4 + i) * OBP + dt * 16 + r] = o[dt][i] * alpha[i];
+      ob[(kg * ATT_QT + g * 4 + i) * OBP + (dh * DTW + dt) * 16 + r] = o[dt][i] * alpha[i];
   // the merged rows' 1 / L and log2-sum-exp, once per row (threads 0..15)
   __shared__ float rinv[ATT_QT], rlse[ATT_QT];
   if (t < ATT_QT) {
@@ -245,11 +285,12 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   __syncthreads();
 
   PI0_PROBE(4);
-  // thread t owns 4 16-byte pieces: piece id = t + 256 j -> row id/64, columns 4*(id%64)..
-  f32x4 acc[4];
+  // thread t owns PPT 16-byte pieces: piece id = t + NT j -> row id/64, columns 4*(id%64)..
+  constexpr int PPT = ATT_QT * 64 / NT;
+  f32x4 acc[PPT];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int id = t + 256 * j, row = id >> 6, col = (id & 63) * 4;
+  for (int j = 0; j < PPT; ++j) {
+    const int id = t + NT * j, row = id >> 6, col = (id & 63) * 4;
     f32x4 v = zero4();
 #pragma unroll
     for (int w = 0; w < 4; ++w) v += *reinterpret_cast<const f32x4*>(&ob[(w * ATT_QT + row) * OBP + col]);
@@ -258,8 +299,8 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
 
   if (a.nchunks == 1) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int id = t + 256 * j, grow = q0 + (id >> 6), col = (id & 63) * 4;
+    for (int j = 0; j < PPT; ++j) {
+      const int id = t + NT * j, grow = q0 + (id >> 6), col = (id & 63) * 4;
       if (grow < a.rows) {
         const bf16x4 pk = {f2bf(acc[j][0]), f2bf(acc[j][1]), f2bf(acc[j][2]), f2bf(acc[j][3])};
         *reinterpret_cast<bf16x4*>(a.out + (size_t)out_row(a, bq, grow) * a.ldo + col) = pk;
@@ -271,8 +312,8 @@ __global__ __launch_bounds__(256, 2) void attn_kernel(AttnArgs a) {
   // ---- several chunks: publish this chunk's normalised partial and log2-sum-exp
   // (plain stores; the kernel boundary orders them before attn_combine_kernel)
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int id = t + 256 * j, prow = q0 + (id >> 6), col = (id & 63) * 4;
+  for (int j = 0; j < PPT; ++j) {
+    const int id = t + NT * j, prow = q0 + (id >> 6), col = (id & 63) * 4;
     *reinterpret_cast<f32x4*>(a.part + ((size_t)c * a.rows_pad + prow) * ATT_HD + col) = acc[j];
     if ((id & 63) == 0) a.lse[(size_t)c * a.rows_pad + prow] = rlse[id >> 6];
   }
@@ -288,30 +329,9 @@ __global__ __launch_bounds__(CMB_THREADS) void attn_combine_kernel(AttnArgs a) {
   const int bq = grow / a.rows, row = grow - bq * a.rows;
   a.part += (size_t)bq * a.nchunks * a.rows_pad * ATT_HD;
   a.lse += (size_t)bq * a.nchunks * a.rows_pad;
-  float lse_c[MAX_CHUNKS];
-  f32x4 pv[MAX_CHUNKS];
-#pragma unroll
-  for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
-    const int ci = min(cc, a.nchunks - 1);
-    lse_c[cc] = a.lse[(size_t)ci * a.rows_pad + row];
-    pv[cc] = *reinterpret_cast<const f32x4*>(a.part + ((size_t)ci * a.rows_pad + row) * ATT_HD + col);
-  }
-  float lmax = NEG_BIG;
-#pragma unroll
-  for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
-    lse_c[cc] = cc < a.nchunks ? lse_c[cc] : NEG_BIG;
-    lmax = fmaxf(lmax, lse_c[cc]);
-  }
-  float wsum = 0.f;
-  f32x4 o4 = zero4();
-#pragma unroll
-  for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
-    const float w = cc < a.nchunks ? fast_exp2(lse_c[cc] - lmax) : 0.f;
-    wsum += w;
-    o4 += w * pv[cc];
-  }
-  const float winv = wsum > 0.f ? __builtin_amdgcn_rcpf(wsum) : 0.f;
-  const bf16x4 pk = {f2bf(o4[0] * winv), f2bf(o4[1] * winv), f2bf(o4[2] * winv), f2bf(o4[3] * winv)};
+  const __amdgpu_buffer_rsrc_t pr = rows_rsrc(a.part, a.nchunks * a.rows_pad * ATT_HD * (int)sizeof(float));
+  const __amdgpu_buffer_rsrc_t lr = rows_rsrc(a.lse, a.nchunks * a.rows_pad * (int)sizeof(float));
+  const bf16x4 pk = merge_piece(pr, lr, a.nchunks, a.rows_pad, row, col);
   *reinterpret_cast<bf16x4*>(a.out + (size_t)out_row(a, bq, row) * a.ldo + col) = pk;
 }
 
@@ -320,6 +340,7 @@ __global__ __launch_bounds__(CMB_THREADS) void attn_combine_kernel(AttnArgs a) {
 using namespace pi0;
 
 static inline size_t round256(size_t v) { return (v + 255) / 256 * 256; }
+
 
 extern "C" size_t pi0hip_attention_batched_workspace_bytes(int rows, int keys, int batch);
 
@@ -382,7 +403,8 @@ static int attention_launch(const void* q, int ldq, const void* k, const void* v
   base += round256((size_t)batch * a.nchunks * a.rows_pad * sizeof(float));
   a.part = reinterpret_cast<float*>(base);
   a.scale_log2 = 1.4426950408889634f / sqrtf((float)head_dim);
-  hipLaunchKernelGGL(attn_kernel, dim3(grid + a.pf_workgroups, batch), dim3(256), 0, s, a);
+  // (8 waves, each with half the head dimension of P @ V, measured slower in the loop)
+  hipLaunchKernelGGL(attn_kernel<4>, dim3(grid + a.pf_workgroups, batch), dim3(256), 0, s, a);
   if (a.nchunks > 1) {
     if (hipError_t e = hipGetLastError()) return (int)e;
     hipLaunchKernelGGL(attn_combine_kernel, dim3((batch * rows * 64 + CMB_THREADS - 1) / CMB_THREADS),
@@ -419,10 +441,10 @@ int pi0hip_attention_prefetch(const void* q, int ldq, const void* k, const void*
                               int head_dim, void* ws, size_t ws_bytes, const void* pf0,
                               size_t pf0_bytes, int pf0_slices, const void* pf1, size_t pf1_bytes,
                               int pf1_slices, const void* pf2, size_t pf2_bytes, int pf2_slices,
-                              hipStream_t s) {
-  const void* ptr[PF_MAX] = {pf0, pf1, pf2};
-  const size_t bytes[PF_MAX] = {pf0_bytes, pf1_bytes, pf2_bytes};
-  const int slices[PF_MAX] = {pf0_slices, pf1_slices, pf2_slices};
+                              const void* pf3, size_t pf3_bytes, int pf3_slices, hipStream_t s) {
+  const void* ptr[PF_MAX] = {pf0, pf1, pf2, pf3};
+  const size_t bytes[PF_MAX] = {pf0_bytes, pf1_bytes, pf2_bytes, pf3_bytes};
+  const int slices[PF_MAX] = {pf0_slices, pf1_slices, pf2_slices, pf3_slices};
   return attention_launch(q, ldq, k, v, ldkv, 0, out, ldo, rows, keys, enc_len, heads, head_dim,
                           1, ws, ws_bytes, PF_MAX, ptr, bytes, slices, s);
 }

@@ -140,8 +140,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int row, int nt
   *reinterpret_cast<bf16x4*>(a.out + (size_t)row * a.ldo + n) = pk;
 }
 
-template <int EPI, bool DUAL, int KTW>
-__global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
+template <int EPI, bool DUAL, int KTW, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void skinny_gemm_kernel(GemmArgs a) {
   constexpr int ND = DUAL ? 2 : 1;
   constexpr bool RMS = uses_rms(EPI);
   constexpr int KW = KTW * 32;            // k columns per wave
@@ -153,8 +153,8 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   constexpr int BRPI = PI0_WAVE / BCH;    // rows per load instruction
   constexpr int OPS = XIB + KB * ND;      // vector-memory ops issued per k-block
   static_assert(NKB <= 4 && 3 * OPS <= 63, "k-block waits");
-  constexpr size_t X_BYTES = 4 * 64 * KW * 2;
-  constexpr size_t R_BYTES = (ND * 4 * 4 * 4 * PI0_WAVE + 4 * 4 * PI0_WAVE) * 4;
+  constexpr size_t X_BYTES = NW * 64 * KW * 2;
+  constexpr size_t R_BYTES = (ND * NW * 4 * 4 * PI0_WAVE + NW * 4 * PI0_WAVE) * 4;
   __shared__ __attribute__((aligned(16))) char smem[X_BYTES > R_BYTES ? X_BYTES : R_BYTES];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -254,8 +254,8 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   PI0_PROBE(4);
   __syncthreads();                        // x staging area becomes the reduction area
 
-  // ---- intra-workgroup reduction over the 4 waves' K ranges
-  typedef float RedT[4][4][4][PI0_WAVE];  // [wave][mt][i][lane]
+  // ---- intra-workgroup reduction over the NW waves' K ranges
+  typedef float RedT[NW][4][4][PI0_WAVE];  // [wave][mt][i][lane]
   RedT* red = reinterpret_cast<RedT*>(smem);
   float (*ssred)[4][PI0_WAVE] = reinterpret_cast<float (*)[4][PI0_WAVE]>(
       smem + ND * sizeof(RedT));
@@ -271,7 +271,8 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   __syncthreads();
 
   PI0_PROBE(5);
-  // thread t owns row t/4 (of 64) and columns 4*(t%4) .. +3 of the tile
+  // thread t < 256 owns row t/4 (of 64) and columns 4*(t%4) .. +3 of the tile
+  if (NW > 4 && t >= 256) return;
   const int lrow = t >> 2, c4 = (t & 3) * 4;
   const int mt = lrow >> 4, r16 = lrow & 15, ii = r16 & 3, gg = r16 >> 2;
   float v0[4], v1[4], ss = 0.f;
@@ -279,7 +280,7 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   for (int c = 0; c < 4; ++c) {
     float s0 = 0.f, s1 = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < NW; ++w) {
       s0 += red[0][w][mt][ii][gg * 16 + c4 + c];
       if constexpr (DUAL) s1 += red[ND - 1][w][mt][ii][gg * 16 + c4 + c];
     }
@@ -287,7 +288,7 @@ __global__ __launch_bounds__(256, 1) void skinny_gemm_kernel(GemmArgs a) {
   }
   if constexpr (RMS) {
 #pragma unroll
-    for (int w = 0; w < 4; ++w)
+    for (int w = 0; w < NW; ++w)
 #pragma unroll
       for (int q = 0; q < 4; ++q) ss += ssred[w][mt][q * 16 + r16];
   }
@@ -384,15 +385,19 @@ static int launch_gemm(const GemmArgs& a, hipStream_t s) {
   const int KT = a.K / 32;
   if (KT % (4 * a.splitk)) return PI0HIP_ERR_SHAPE;
   if (a.splitk > 1 && !a.ws) return PI0HIP_ERR_WORKSPACE;
-  const int ktw = KT / (4 * a.splitk);
+  // 4 waves split the workgroup's K range (8 or 16 waves with fewer loads each measured
+  // slower: the cross-wave reduction grows with the wave count)
+  constexpr int nw = 4;
+  const int kts = KT / a.splitk;
+  const int ktw = kts / nw;
   dim3 grid((a.N / 16) * a.splitk, (a.M + 63) / 64);
-  switch (ktw) {
-    case 1: skinny_gemm_kernel<EPI, DUAL, 1><<<grid, 256, 0, s>>>(a); break;
-    case 2: skinny_gemm_kernel<EPI, DUAL, 2><<<grid, 256, 0, s>>>(a); break;
-    case 4: skinny_gemm_kernel<EPI, DUAL, 4><<<grid, 256, 0, s>>>(a); break;
-    case 8: skinny_gemm_kernel<EPI, DUAL, 8><<<grid, 256, 0, s>>>(a); break;
-    default: return PI0HIP_ERR_SHAPE;
-  }
+#define PI0_SKINNY(KTW_, NW_) skinny_gemm_kernel<EPI, DUAL, KTW_, NW_><<<grid, NW_ * 64, 0, s>>>(a)
+  if (ktw == 1) PI0_SKINNY(1, 4);
+  else if (ktw == 2) PI0_SKINNY(2, 4);
+  else if (ktw == 4) PI0_SKINNY(4, 4);
+  else if (ktw == 8) PI0_SKINNY(8, 4);
+  else return PI0HIP_ERR_SHAPE;
+#undef PI0_SKINNY
   if (a.splitk > 1) {
     if (hipError_t e = hipGetLastError()) return (int)e;
     const dim3 rgrid(a.N / 16, (a.M + 63) / 64 * (256 / RED_THREADS));
@@ -407,6 +412,123 @@ static int launch_gemm(const GemmArgs& a, hipStream_t s) {
   return (int)hipGetLastError();
 }
 
+
+// Row-split GEMM: out[M, N] (+)= x[M, K] @ W[K, N] (+ epilogue) in one launch, no split-K.
+// Workgroup = 16 rows x 16 columns over the whole K; its NW waves split K and are summed
+// through LDS. With M = 51 and N = 1024 that is 4 row blocks x 64 column tiles = 256
+// workgroups, so the chip fills without fp32 partials and without a second (reduce)
+// launch. Each wave copies its x slice (16 rows x K / NW) from L2 straight into LDS with
+// loads that each read whole contiguous row segments (a load whose 16 lanes sit on 16
+// rows 2-8 KB apart is ~2x slower), 16-byte chunks XOR-swizzled by row so the A-fragment
+// reads are free of bank conflicts; the packed B fragments go to registers. The 4 row
+// blocks of a column tile are placed on one XCD (workgroup b runs on XCD b % 8), so its
+// weight tile crosses HBM once and the other three read it from that XCD's L2.
+template <int EPI, int KTW, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void rows16_kernel(GemmArgs a, int nrb, int xcd_map) {
+  constexpr int KW = KTW * 32;                 // k per wave
+  constexpr int CPR = KW / 8;                  // 16-byte chunks per row of the wave's slice
+  constexpr int RPI = PI0_WAVE / CPR;          // rows per load instruction
+  constexpr int XI = 16 / RPI;                 // load instructions per wave
+  constexpr int SWM = (CPR < 16 ? CPR : 16) - 1;
+  constexpr bool RMS = uses_rms(EPI), PRE = uses_prescale(EPI);
+  static_assert(RPI >= 1 && RPI * CPR == PI0_WAVE && XI * RPI == 16, "slice shape");
+  static_assert(EPI == EPI_RES || EPI == EPI_BIAS || EPI == EPI_RMS_BIAS_RES ||
+                EPI == EPI_RMS_BIAS_RES_PRE, "row-split epilogues");
+  // (EPI_BIAS and the Euler out-projection epilogues were measured on the small per-step
+  // projections too: 0.02 ms per chunk, below box-to-box noise, so only EPI_RES ships)
+  constexpr size_t X_BYTES = (size_t)NW * 16 * KW * 2;
+  __shared__ __attribute__((aligned(16))) char smem[X_BYTES];
+  __shared__ float ssw[NW][16];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int KT = a.K >> 5;
+  int nt, rb;
+  if (xcd_map) {            // column tiles congruent to the XCD index, all row blocks each
+    const int b = blockIdx.x, xcd = b & 7, j = b >> 3;
+    nt = (j / nrb) * 8 + xcd;
+    rb = j - (j / nrb) * nrb;
+  } else {
+    nt = blockIdx.x / nrb;
+    rb = blockIdx.x - nt * nrb;
+  }
+  const int m0 = rb * 16, rows = min(16, a.M - m0);
+  const int kt0 = wave * KTW;
+  const int r = lane & 15, g = lane >> 4;
+  float fpre = 1.f;
+  if constexpr (PRE) fpre = bf2f(a.prescale[m0 + min(r, rows - 1)]);
+  // bounded resource over this row block: rows past M read as zeros
+  const __amdgpu_buffer_rsrc_t xr =
+      rows_rsrc_sgpr(a.x + (size_t)m0 * a.ldx, rows * a.ldx * (int)sizeof(__bf16));
+  char* xs = smem + (size_t)wave * 16 * KW * 2;
+  {
+    const int lrow = lane / CPR, c = lane % CPR;
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+      const int row = i * RPI + lrow;
+      // LDS slot (row, c) receives global chunk c ^ swz(row)
+      buf_load16_lds(xr, xs + i * 1024,
+                     (row * a.ldx + kt0 * 32 + ((c ^ (row & SWM)) * 8)) * (int)sizeof(__bf16));
+    }
+  }
+  const __bf16* wq = a.w0 + ((size_t)nt * KT + kt0) * 512 + lane * 8;
+  bf16x8 bv[KTW];
+#pragma unroll
+  for (int i = 0; i < KTW; ++i) bv[i] = load8(wq + i * 512);
+  __builtin_amdgcn_s_waitcnt(PI0_VMCNT(0));    // this wave's LDS copies and fragments
+  __builtin_amdgcn_sched_barrier(0);
+  f32x4 acc = zero4();
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < KTW; ++i) {
+    const int ch = (i * 4 + g) ^ (r & SWM);
+    bf16x8 av = *reinterpret_cast<const bf16x8*>(xs + (r * CPR + ch) * 16);
+    if constexpr (RMS) {     // the row's sum of squares from the same fragments
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bf16x2 q = {av[2 * e], av[2 * e + 1]};
+        ss = __builtin_amdgcn_fdot2_f32_bf16(q, q, ss, false);
+      }
+    }
+    if constexpr (PRE) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) av[e] = f2bf(bf2f(av[e]) * fpre);
+    }
+    acc = mfma16(av, bv[i], acc);
+  }
+  if constexpr (RMS) {
+    ss += __shfl_xor(ss, 16, PI0_WAVE);
+    ss += __shfl_xor(ss, 32, PI0_WAVE);
+    if (g == 0) ssw[wave][r] = ss;
+  }
+  __syncthreads();                             // every wave is done with its x slice
+  float (*red)[4][PI0_WAVE] = reinterpret_cast<float (*)[4][PI0_WAVE]>(smem);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) red[wave][i][lane] = acc[i];
+  __syncthreads();
+  // thread t: row t / 16, column t % 16; C lane (row / 4) * 16 + col holds element row % 4
+  const int row = t >> 4, col = t & 15;
+  if (t >= 256 || row >= rows) return;
+  const int l = (row >> 2) * 16 + col, i = row & 3;
+  float v = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) v += red[w][i][l];
+  const int n = nt * 16 + col;
+  const size_t o = (size_t)(m0 + row) * a.ldo + n;
+  if constexpr (EPI == EPI_RES) {
+    a.out[o] = f2bf(v + bf2f(a.out[o]));
+  } else if constexpr (EPI == EPI_BIAS) {
+    a.out[o] = f2bf(v + bf2f(a.bias[n]));
+  } else {
+    float f = 1.f;
+    if constexpr (RMS) {
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) sum += ssw[w][row];
+      f = round_bf(rsqrtf(sum / (float)a.K + 1e-6f));
+    }
+    if (a.out_f32) a.out_f32[o] += v * f + bf2f(a.bias[n]);   // fp32 Euler accumulator
+    else a.out[o] = f2bf(v * f + bf2f(a.bias[n]) + bf2f(a.out[o]));
+  }
+}
 
 // W[batch][K][N] row-major -> packed B fragments, one thread per 16-byte fragment row.
 __global__ void pack_weight_kernel(const __bf16* __restrict__ w, __bf16* __restrict__ p,
@@ -433,7 +555,28 @@ __global__ void pack_weight_kernel(const __bf16* __restrict__ w, __bf16* __restr
 
 using namespace pi0;
 
+
 static inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+template <int EPI>
+static int launch_rows(const GemmArgs& a, hipStream_t s) {
+  if (!a.x || !a.w0 || !(a.out || a.out_f32) || a.M <= 0 || a.N <= 0 || a.K <= 0)
+    return PI0HIP_ERR_ARG;
+  if (a.N % 16 || a.ldx < a.K || (a.ldx & 7) || (reinterpret_cast<uintptr_t>(a.x) & 15))
+    return PI0HIP_ERR_SHAPE;
+  const int nrb = (a.M + 15) / 16, ntiles = a.N / 16;
+  const int grid = nrb * ntiles;
+  const int xcd_map = ntiles % 8 == 0;
+  // 8 waves split K (at most 16 fragments of W in registers per wave)
+  switch (a.K) {
+    case 512: rows16_kernel<EPI, 2, 8><<<grid, 512, 0, s>>>(a, nrb, xcd_map); break;
+    case 1024: rows16_kernel<EPI, 4, 8><<<grid, 512, 0, s>>>(a, nrb, xcd_map); break;
+    case 2048: rows16_kernel<EPI, 8, 8><<<grid, 512, 0, s>>>(a, nrb, xcd_map); break;
+    case 4096: rows16_kernel<EPI, 16, 8><<<grid, 512, 0, s>>>(a, nrb, xcd_map); break;
+    default: return PI0HIP_ERR_SHAPE;
+  }
+  return (int)hipGetLastError();
+}
 
 extern "C" {
 
@@ -491,6 +634,11 @@ int pi0hip_linear_residual(const void* x, int ldx, const void* wp, void* out, in
   GemmArgs a = base_args(x, ldx, wp, out, ldo, M, N, K, splitk);
   if (int e = setup_ws(a, ws, ws_bytes, 0)) return e;
   return launch_gemm<EPI_RES, false>(a, s);
+}
+
+int pi0hip_linear_residual_rows(const void* x, int ldx, const void* wp, void* out, int ldo,
+                                int M, int N, int K, hipStream_t s) {
+  return launch_rows<EPI_RES>(base_args(x, ldx, wp, out, ldo, M, N, K, 1), s);
 }
 
 int pi0hip_rms_linear_bias_residual(const void* x, int ldx, const void* wp, const void* bias,

@@ -27,6 +27,7 @@ PROTOTYPES = {
                                    P, c_size_t, P]),
     "pi0hip_linear_residual": (c_int, [P, c_int, P, P, c_int, c_int, c_int, c_int, c_int,
                                        P, c_size_t, P]),
+    "pi0hip_linear_residual_rows": (c_int, [P, c_int, P, P, c_int, c_int, c_int, c_int, P]),
     "pi0hip_rms_linear_bias_residual": (c_int, [P, c_int, P, P, P, c_int, c_int, c_int, c_int,
                                                 c_int, P, c_size_t, P]),
     "pi0hip_norm_qkv_rope": (c_int, [P, c_int, P, P, P, P, P, c_int, P, c_int, c_int, c_int,
@@ -52,7 +53,8 @@ PROTOTYPES = {
                                          c_int, c_int, c_int, c_int, c_int, P, c_size_t, P]),
     "pi0hip_attention_prefetch": (c_int, [P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int,
                                           c_int, c_int, P, c_size_t, P, c_size_t, c_int, P,
-                                          c_size_t, c_int, P, c_size_t, c_int, P]),
+                                          c_size_t, c_int, P, c_size_t, c_int, P, c_size_t, c_int,
+                                          P]),
     "pi0hip_tile_qkv_rope_batched": (c_int, [P, c_int, P, P, P, P, P, c_int, ctypes.c_longlong,
                                              c_int, c_int, c_int, c_int, c_int, P]),
     "pi0hip_encoder_attention_batched_workspace_bytes": (c_size_t, [c_int, c_int]),

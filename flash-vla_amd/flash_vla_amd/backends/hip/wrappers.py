@@ -99,6 +99,8 @@ class _PackedEntry:
         return owner.as_strided(shape, stride, offset)
 
     def _drop(self, _ref) -> None:
+        if _PACKED is None:           # interpreter shutdown: module globals already cleared
+            return
         try:
             _PACKED.remove(self)
         except ValueError:
@@ -332,16 +334,29 @@ def decoder_attention(Q, K, V, scores, out, encoder_seq_len):
     return out
 
 
-def decoder_attention_prefetch(Q, K, V, scores, out, encoder_seq_len, gate_w, up_w, down_w):
-    """`decoder_attention` whose spare workgroups also pull this layer's gate / up / down
-    weights into the L2 of the XCDs that will read them (pi0hip_attention_prefetch).
+# regions the attention launch prefetches: the o-proj that follows it, then the FFN
+PREFETCH_OPROJ = True
+
+
+def _consumer_slices(M: int, w) -> int:
+    """Slices of packed `w` such that slice s is what workgroup s of its residual GEMM reads
+    (and so lands on XCD s % 8): row-split -> one column tile per slice (the tile's
+    workgroups sit on XCD nt % 8); split-K -> the (N / 16) x splitk K-slices."""
+    Kw, Nw = w.shape
+    return (Nw // 16) * (1 if RESIDUAL_MODE == "rows" else _splitk(M, Nw, Kw))
+
+
+def decoder_attention_prefetch(Q, K, V, scores, out, encoder_seq_len, gate_w, up_w, down_w,
+                               o_w=None):
+    """`decoder_attention` whose spare workgroups also pull this layer's o-proj, gate / up
+    and down weights into the L2 of the XCDs that will read them (pi0hip_attention_prefetch).
 
     Engine-level option of this backend, not a reference call site: the reference's
     decoder_attention (fused_wrappers.py:88-115) prefetches nothing. The result is bitwise
     that of decoder_attention. Used for one request whose GEMMs take the skinny kernels,
-    where workgroup s of the gate / up launch reads packed tile s and workgroup s of the
-    split-K down launch reads the s-th of its (N / 16) x splitk K-slices; otherwise it
-    is plain decoder_attention."""
+    where workgroup s of the gate / up launch reads packed tile s and the residual GEMMs'
+    workgroups read the slices `_consumer_slices` describes; otherwise it is plain
+    decoder_attention."""
     rows = Q.shape[0]
     M = rows // DECODER_HEADS
     if K.dim() == 3 or M > _TILE_M:
@@ -352,9 +367,13 @@ def decoder_attention_prefetch(Q, K, V, scores, out, encoder_seq_len, gate_w, up
             or K.stride(0) != V.stride(0)):
         raise ValueError("decoder_attention: shape mismatch")
     regions = []
-    for w, splitk in ((gate_w, 1), (up_w, 1), (down_w, 0)):     # 0: the down's split-K count
-        Kw, Nw = w.shape
-        regions += [packed_weight_ptr(w), Kw * Nw * 2, (Nw // 16) * (splitk or _splitk(M, Nw, Kw))]
+    if o_w is not None and PREFETCH_OPROJ:
+        regions += [packed_weight_ptr(o_w), o_w.numel() * 2, _consumer_slices(M, o_w)]
+    else:
+        regions += [None, 0, 0]
+    for w in (gate_w, up_w):
+        regions += [packed_weight_ptr(w), w.numel() * 2, w.shape[1] // 16]
+    regions += [packed_weight_ptr(down_w), down_w.numel() * 2, _consumer_slices(M, down_w)]
     lib = _abi.lib()
     nbytes = lib.pi0hip_attention_batched_workspace_bytes(rows, keys, 1)
     ws = scratch("attn_ws", (nbytes,), torch.uint8, Q.device)
@@ -374,12 +393,27 @@ def attention_prefetch_for(attention_op):
 _TILE_M = 64
 
 
+def _rows_ok(x, K: int, N: int) -> bool:
+    """The row-split kernel's shape rules (pi0hip_linear_residual_rows)."""
+    return (RESIDUAL_MODE == "rows" and x.shape[0] <= _TILE_M and K in (512, 1024, 2048, 4096)
+            and N % 16 == 0 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0)
+
+
+# Residual GEMMs at M <= 64: "rows" = one launch of 16-row workgroups over the whole K
+# (pi0hip_linear_residual_rows); "splitk" = split-K partials + a reduce launch.
+RESIDUAL_MODE = "rows"
+
+
 def _residual(x, weight, out, role):
     _check(x, "x", 2); _check(out, "out", 2)
     M, K = x.shape
     N = weight.shape[1]
     if weight.shape[0] != K or out.shape != (M, N):
         raise ValueError(f"{role}: shape mismatch")
+    if _rows_ok(x, K, N):
+        _abi.call("pi0hip_linear_residual_rows", _ptr(x), x.stride(0), packed_weight_ptr(weight),
+                  _ptr(out), out.stride(0), M, N, K, _stream())
+        return out
     if M > _TILE_M and K % 256 == 0 and N % 128 == 0:
         s = 4
         nbytes = _abi.lib().pi0hip_tile_workspace_bytes(M, N, s)

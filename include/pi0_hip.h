@@ -130,20 +130,20 @@ int pi0hip_attention_batched(const void* q, int ldq, const void* k, const void* 
 
 /* pi0hip_attention (one request) plus an L2 prefetch for the launches that follow it:
  * spare workgroups (filling the chip to two per CU next to the attention's) touch
- * every 128-byte line of up to three regions, region r being pfr_slices equal slices
+ * every 128-byte line of up to four regions, region r being pfr_slices equal slices
  * of pfr_bytes in all, where slice s is what workgroup s of the consuming launch reads
  * (workgroup s runs on XCD s % 8, so the slice lands in that XCD's L2). A null region
  * is skipped; pfr_bytes / pfr_slices must be a multiple of 128, pfr 4-byte aligned.
  * Loads only: `out` is bitwise that of pi0hip_attention. No reference counterpart
  * (the reference's decoder_attention, fused_wrappers.py:88-115, launches no prefetch);
- * the decoder engine passes the layer's gate / up / down weights (their skinny GEMM
- * launches read slice s in workgroup s), which brings the loop ~6% per chunk. */
+ * the decoder engine passes the layer's o-proj, gate / up and down weights (their
+ * launches read slice s on XCD s % 8). */
 int pi0hip_attention_prefetch(const void* q, int ldq, const void* k, const void* v, int ldkv,
                               void* out, int ldo, int rows, int keys, int enc_len, int heads,
                               int head_dim, void* ws, size_t ws_bytes, const void* pf0,
                               size_t pf0_bytes, int pf0_slices, const void* pf1, size_t pf1_bytes,
                               int pf1_slices, const void* pf2, size_t pf2_bytes, int pf2_slices,
-                              hipStream_t s);
+                              const void* pf3, size_t pf3_bytes, int pf3_slices, hipStream_t s);
 
 /* out = softmax(mask(q k^T / sqrt(head_dim))) v over `keys` cache rows; flat
  * query row r = token * heads + head; rows r < heads keep keys j <= enc_len.
@@ -153,6 +153,14 @@ int pi0hip_attention_prefetch(const void* q, int ldq, const void* k, const void*
 int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int ldkv, void* out,
                      int ldo, int rows, int keys, int enc_len, int heads, int head_dim,
                      void* ws, size_t ws_bytes, hipStream_t s);
+
+/* out[M, N] += x[M, K] @ w[K, N] in one launch: 16-row x 16-column workgroups over the
+ * whole K (no split-K partials, no reduce launch). Packed w; K in {512, 1024, 2048, 4096},
+ * N % 16 == 0, x 16-byte aligned with ldx % 8 == 0.
+ * decoder_out_proj_residual wrappers.py:176-181, decoder_ffn_down_residual
+ * wrappers.py:184-189 (tl_matmul_res, kernels/base.py:115-154) */
+int pi0hip_linear_residual_rows(const void* x, int ldx, const void* w_packed, void* out, int ldo,
+                                int M, int N, int K, hipStream_t s);
 
 /* ---- unfused decoder call sites (op_table(fused=False)) ------------------------
  * The reference's two-kernel decoder path, kept for its rounding points: the RMS

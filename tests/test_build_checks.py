@@ -36,7 +36,7 @@ def test_kblock_waits_hold(gemm_asm):
 
 
 def test_kblock_waits_reject_a_loose_wait(gemm_asm):
-    name = "_ZN3pi018skinny_gemm_kernelILi4ELb1ELi8EEEvNS_8GemmArgsE"
+    name = "_ZN3pi018skinny_gemm_kernelILi4ELb1ELi8ELi4EEEvNS_8GemmArgsE"
     start = gemm_asm.index(name + ":")
     body = gemm_asm[start:gemm_asm.index("s_endpgm", start)]
     first = body.index("s_waitcnt vmcnt(")

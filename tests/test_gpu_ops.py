@@ -144,6 +144,22 @@ def test_attention_state_rows_ignore_action_keys():
     assert not torch.equal(outs[0][8:], outs[1][8:])
 
 
+@pytest.mark.parametrize("M,K,N", [(1, 512, 1024), (16, 1024, 1024), (17, 2048, 32),
+                                   (51, 4096, 1024), (64, 4096, 48), (50, 2048, 1024)])
+def test_residual_rows_kernel_shapes(M, K, N):
+    """The row-split residual GEMM (one launch, 16-row workgroups over the whole K) at its
+    edges: a single row, exact and ragged 16-row blocks, column counts that are and are not
+    a multiple of 8 tiles (the XCD placement applies only to the former)."""
+    from flash_vla_amd.backends.hip import _abi
+    x, w, r = rnd((M, K), 121), rnd((K, N), 122, 0.02), rnd((M, N), 123)
+    out = r.to(DEV).clone()
+    xd, wd = x.to(DEV), w.to(DEV)          # the packed copy lives as long as wd
+    _abi.call("pi0hip_linear_residual_rows", xd.data_ptr(), K, W.packed_weight_ptr(wd),
+              out.data_ptr(), N, M, N, K, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    close(out, O.op_matmul_residual(x.float(), w.float(), r.float()), what=f"rows M={M} K={K}")
+
+
 @pytest.mark.parametrize("M,K", [(51, 2048), (51, 4096), (204, 2048), (204, 4096), (100, 4096)])
 def test_residual_gemm(M, K):
     """M > 64 (the batched decoder) runs on the tile kernel's split-K path."""
