@@ -23,6 +23,8 @@
 #include "pi0_common.h"
 #include "pi0_hip.h"
 
+#include <mutex>
+
 namespace pi0 {
 
 constexpr int ATT_HD = 256;
@@ -454,6 +456,53 @@ int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int l
                      void* ws, size_t ws_bytes, hipStream_t s) {
   return pi0hip_attention_batched(q, ldq, k, v, ldkv, 0, out, ldo, rows, keys, enc_len, heads,
                                   head_dim, 1, ws, ws_bytes, s);
+}
+
+}  // extern "C"
+
+// ---- allocation-free variant --------------------------------------------------------
+// The attention's workspace (per-chunk partial outputs and log2-sum-exps) lives in a
+// file-scope device array; every GPU the library runs on holds its own copy until the
+// process ends. Host code must not use the array's name as a device address: its address
+// on the current device comes from hipGetSymbolAddress, fetched once per device and cached.
+constexpr size_t ATT_NOALLOC_SCRATCH_BYTES = size_t(8) << 20;
+static __device__ __align__(256) char scratch[ATT_NOALLOC_SCRATCH_BYTES];
+
+static constexpr int MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[MAX_DEVICES];
+
+static int scratch_address(void** out) {
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev)) return (int)e;
+  if (dev < 0 || dev >= MAX_DEVICES) return PI0HIP_ERR_ARG;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) return (int)e;
+    if (!p) return PI0HIP_ERR_WORKSPACE;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+extern "C" {
+
+size_t pi0hip_attention_noalloc_max_bytes(void) { return ATT_NOALLOC_SCRATCH_BYTES; }
+
+int pi0hip_attention_noalloc(const void* q, int ldq, const void* k, const void* v, int ldkv,
+                             void* out, int ldo, int rows, int keys, int enc_len, int heads,
+                             int head_dim, hipStream_t s) {
+  if (rows <= 0 || keys <= 0) return PI0HIP_ERR_ARG;
+  const size_t need = pi0hip_attention_batched_workspace_bytes(rows, keys, 1);
+  if (need > ATT_NOALLOC_SCRATCH_BYTES) return PI0HIP_ERR_WORKSPACE;
+  void* ws = nullptr;
+  if (int e = scratch_address(&ws)) return e;
+  // every byte the kernels read from the workspace is written earlier in the same call, so
+  // nothing needs clearing; the contents left by the previous call are simply overwritten
+  return attention_launch(q, ldq, k, v, ldkv, 0, out, ldo, rows, keys, enc_len, heads, head_dim,
+                          1, ws, ATT_NOALLOC_SCRATCH_BYTES, 0, nullptr, nullptr, nullptr, s);
 }
 
 }  // extern "C"

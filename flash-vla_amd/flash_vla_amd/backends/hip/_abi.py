@@ -36,6 +36,9 @@ PROTOTYPES = {
     "pi0hip_attention_workspace_bytes": (c_size_t, [c_int, c_int]),
     "pi0hip_attention": (c_int, [P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int, c_int,
                                  c_int, P, c_size_t, P]),
+    "pi0hip_attention_noalloc_max_bytes": (c_size_t, []),
+    "pi0hip_attention_noalloc": (c_int, [P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int,
+                                         c_int, c_int, P]),
     # unfused decoder call sites
     "pi0hip_rms_factor": (c_int, [P, c_int, P, c_int, c_int, P]),
     "pi0hip_scaled_gated_ffn": (c_int, [P, c_int, P, P, P, P, c_int, c_int, c_int, c_int, P]),

@@ -205,6 +205,18 @@ int pi0hip_attention_unfused(const void* q, int ldq, const void* k, const void* 
                              int ldo, int rows, int keys, int enc_len, int heads, int head_dim,
                              hipStream_t s);
 
+/* pi0hip_attention without a workspace argument and without any allocation: the
+ * partial outputs live in a static per-device array of pi0hip_attention_noalloc_max_bytes()
+ * (8 MiB), enough for pi0hip_attention_workspace_bytes(rows, keys) up to e.g. 408 rows x
+ * 2048 keys; larger shapes return PI0HIP_ERR_WORKSPACE without launching. Calls that
+ * overlap on one GPU (several streams or threads at once) share the array and race.
+ * No counterpart in the reference: for callers that cannot allocate device memory
+ * (code under graph capture that may not call hipMalloc, tight serving loops). */
+size_t pi0hip_attention_noalloc_max_bytes(void);
+int pi0hip_attention_noalloc(const void* q, int ldq, const void* k, const void* v, int ldkv,
+                             void* out, int ldo, int rows, int keys, int enc_len, int heads,
+                             int head_dim, hipStream_t s);
+
 /* ---- prefix encoder (M = 768..816 token rows, width 2048) --------------------
  * LDS-tiled MFMA GEMMs for the MFMA-bound encoder shapes (32x32x16 MFMAs);
  * weights packed by pi0hip_pack_weight32, K % 128 == 0; activation / output rows
