@@ -138,7 +138,16 @@ def packed_weight_ptr(w: torch.Tensor, layout: int = 16, pad: tuple | None = Non
             pad = None if pad == (K, N) else pad
         if pad is not None and (pad[0] < K or pad[1] < N):
             raise ValueError("padding smaller than the weight")
-    scale = 1 if pad is None else (pad[0] * pad[1]) / (K * N)
+    def packed_offset(byte_off: int) -> int:
+        """Byte offset in the packed copy of the weight at `byte_off` in the source stack:
+        the same for unpadded layouts; for padded ones layer i of [L, K, N] starts at
+        i * K_pad * N_pad elements (integer arithmetic: a float ratio can land a byte off)."""
+        if pad is None:
+            return byte_off
+        layer_bytes = K * N * w.element_size()
+        if byte_off % layer_bytes:
+            raise ValueError("a padded weight must be a whole layer of its stack")
+        return byte_off // layer_bytes * pad[0] * pad[1] * w.element_size()
     ptr = w.data_ptr()
     for e in _PACKED:
         if (e.K == K and e.N == N and e.layout == layout and e.pad == pad
@@ -149,7 +158,7 @@ def packed_weight_ptr(w: torch.Tensor, layout: int = 16, pad: tuple | None = Non
             if not _capturing() and e.version != src._version:
                 _pack_into(src, e.packed, K, N, layout, pad)
                 e.version = src._version
-            return e.packed.data_ptr() + int((ptr - e.base) * scale)
+            return e.packed.data_ptr() + packed_offset(ptr - e.base)
     if _capturing():
         raise RuntimeError("weight was not packed before graph capture; run a warmup pass first")
     base = w._base if w._base is not None else w
@@ -163,7 +172,7 @@ def packed_weight_ptr(w: torch.Tensor, layout: int = 16, pad: tuple | None = Non
     _pack_into(src, packed, K, N, layout, pad)
     entry = _PackedEntry(src, packed, K, N, layout, pad)
     _PACKED.append(entry)
-    return packed.data_ptr() + int((ptr - entry.base) * scale)
+    return packed.data_ptr() + packed_offset(ptr - entry.base)
 
 
 def prepare_weights(weights: dict) -> None:

@@ -136,6 +136,16 @@ def test_large_m_vision_gemms(views):
     close(out.reshape(M, 1152), ref.bfloat16().float(), what=f"vision ffn_down M={M}")
 
 
+def test_padded_layer_views_resolve_exactly():
+    """Layer views of a zero-padded packed stack land exactly on layer boundaries of the
+    packed copy (a float ratio of padded / unpadded sizes put layers 3, 6, 11-13 and 21-26
+    of the 27-layer vision FFN one byte off: misaligned bf16, NaN outputs)."""
+    stack = rnd((27, 1152, 4304), 84, 0.02).to(DEV)
+    base = W.packed_weight_ptr(stack[0], 32, (1152, 4352))
+    for i in (1, 3, 6, 13, 26):
+        assert W.packed_weight_ptr(stack[i], 32, (1152, 4352)) == base + i * 1152 * 4352 * 2
+
+
 def test_ffn_down_ragged_k():
     """K = 4304: the packed weight's zero rows 4304..4351 meet the next row's values."""
     h, w, b, r = rnd((3, 256, 4304), 79, 0.5), rnd((4304, 1152), 80, 0.02), rnd(1152, 81), rnd((3, 256, 1152), 82)
