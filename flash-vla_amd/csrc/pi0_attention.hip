@@ -35,7 +35,7 @@ constexpr int VP = ATT_HD + 16;     // bf16 pitch of staged V rows (544 B: 4 row
 constexpr int OBP = ATT_HD + 4;     // fp32 pitch of the per-wave O buffer
 constexpr float NEG_BIG = -1.0e30f;
 constexpr int MAX_CHUNKS = 16;      // keys <= 2048 (prompts up to 1229 tokens with 3 views)
-constexpr int PF_MAX = 4;           // prefetch regions
+constexpr int PF_MAX = PF_REGIONS;  // prefetch regions
 
 struct AttnArgs {
   const __bf16* q; int ldq;
@@ -46,38 +46,8 @@ struct AttnArgs {
   float scale_log2;
   int batch;                 // requests (grid.y); request b reads K / V at b * kv_bstride
   long long kv_bstride;
-  // optional L2 prefetch by spare workgroups (blockIdx.x >= work_grid, batch 1):
-  // region r is pf_nslices[r] slices of pf_slice_words[r] dwords; slice s is what
-  // workgroup s of the launch that consumes it reads, so it runs on XCD s % 8
-  int work_grid, pf_workgroups, pf_n;
-  const unsigned* pf_base[PF_MAX];
-  int pf_slice_words[PF_MAX], pf_nslices[PF_MAX];
+  L2Prefetch pf;              // optional L2 prefetch by spare workgroups (batch 1)
 };
-
-// Spare workgroup: touch one dword of every 128-byte line of the slices that will be
-// read on this workgroup's XCD (workgroup b of a launch runs on XCD b % 8), pulling
-// them into that XCD's L2 while the attention runs on the other CUs. Loads only;
-// the sum is kept alive by an empty asm statement, nothing is stored.
-__device__ __forceinline__ void prefetch_slices(const AttnArgs& a) {
-  const int p = blockIdx.x, x = p & 7, t = threadIdx.x;
-  const int k0 = (x - a.work_grid % 8 + 8) % 8;          // first spare workgroup on XCD x
-  if (a.pf_workgroups <= k0) return;
-  const int j = (p - a.work_grid - k0) / 8;             // its index there ...
-  const int per_xcd = (a.pf_workgroups - k0 + 7) / 8;   // ... and their number
-  unsigned acc = 0;
-#pragma unroll
-  for (int r = 0; r < PF_MAX; ++r) {     // constant indices: the argument arrays stay in SGPRs
-    if (r >= a.pf_n) break;
-    const int lines = a.pf_slice_words[r] / 32;
-    const int items = (a.pf_nslices[r] - x + 7) / 8 * lines;
-    const unsigned* base = a.pf_base[r];
-    for (int it = j * (int)blockDim.x + t; it < items; it += per_xcd * (int)blockDim.x) {
-      const int sl = x + 8 * (it / lines), l = it - (it / lines) * lines;
-      acc += base[(size_t)sl * a.pf_slice_words[r] + l * 32];
-    }
-  }
-  asm volatile("" ::"v"(acc));
-}
 
 // Output row of local flat row lr (= token * heads + head) of request b: the tokens of a
 // batch are stored "states first" (B state tokens, then B x T action tokens), the order
@@ -138,8 +108,8 @@ __global__ __launch_bounds__(NWV * 64, 2) void attn_kernel(AttnArgs a) {
   static_assert(4 * ATT_QT * OBP * sizeof(float) <= sizeof(kv_), "O buffer");
   __shared__ float sm[4][ATT_QT], sl[4][ATT_QT];
 
-  if ((int)blockIdx.x >= a.work_grid) {
-    prefetch_slices(a);
+  if ((int)blockIdx.x >= a.pf.work_grid) {
+    prefetch_slices(a.pf);
     return;
   }
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -346,21 +316,6 @@ static inline size_t round256(size_t v) { return (v + 255) / 256 * 256; }
 
 extern "C" size_t pi0hip_attention_batched_workspace_bytes(int rows, int keys, int batch);
 
-// CUs of the current device (cached per device): the prefetch fills the chip to two
-// workgroups per CU, the attention kernel's occupancy.
-static int device_cus() {
-  static int cached[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 static int attention_launch(const void* q, int ldq, const void* k, const void* v, int ldkv,
                             long long kv_bstride, void* out, int ldo, int rows, int keys,
                             int enc_len, int heads, int head_dim, int batch, void* ws,
@@ -386,27 +341,17 @@ static int attention_launch(const void* q, int ldq, const void* k, const void* v
   a.rows_pad = nqt * ATT_QT;
   a.nqt = nqt;
   const int grid = nqt * a.nchunks;
-  a.work_grid = grid;
-  for (int r = 0; r < npf; ++r) {          // prefetch regions (null pointers are skipped)
-    if (!pf_ptr[r]) continue;
-    const size_t b = pf_bytes[r];
-    const int n = pf_slices[r];
-    if (n <= 0 || b == 0 || b % n || (b / n) % 128 || b / n / 4 > (size_t)INT32_MAX ||
-        (reinterpret_cast<uintptr_t>(pf_ptr[r]) & 3))
-      return PI0HIP_ERR_SHAPE;
-    a.pf_base[a.pf_n] = static_cast<const unsigned*>(pf_ptr[r]);
-    a.pf_slice_words[a.pf_n] = static_cast<int>(b / n / 4);
-    a.pf_nslices[a.pf_n] = n;
-    ++a.pf_n;
-  }
-  a.pf_workgroups = a.pf_n ? max(0, 2 * device_cus() - grid) : 0;
+  // spare workgroups fill the chip to two per CU, the attention kernel's occupancy
+  if (!make_l2_prefetch(a.pf, grid, max(0, 2 * device_cus() - grid), npf, pf_ptr, pf_bytes,
+                        pf_slices))
+    return PI0HIP_ERR_SHAPE;
   char* base = reinterpret_cast<char*>(ws);
   a.lse = reinterpret_cast<float*>(base);
   base += round256((size_t)batch * a.nchunks * a.rows_pad * sizeof(float));
   a.part = reinterpret_cast<float*>(base);
   a.scale_log2 = 1.4426950408889634f / sqrtf((float)head_dim);
   // (8 waves, each with half the head dimension of P @ V, measured slower in the loop)
-  hipLaunchKernelGGL(attn_kernel<4>, dim3(grid + a.pf_workgroups, batch), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(attn_kernel<4>, dim3(grid + a.pf.workgroups, batch), dim3(256), 0, s, a);
   if (a.nchunks > 1) {
     if (hipError_t e = hipGetLastError()) return (int)e;
     hipLaunchKernelGGL(attn_combine_kernel, dim3((batch * rows * 64 + CMB_THREADS - 1) / CMB_THREADS),

@@ -101,4 +101,75 @@ __device__ __forceinline__ float warp_sum(float v) {
   return v;
 }
 
+// ---- L2 prefetch by spare workgroups ------------------------------------------------
+// A launch may carry extra workgroups (blockIdx.x >= work_grid) that only touch one dword
+// of every 128-byte line of up to PF_REGIONS regions, so that a later launch finds those
+// lines in L2. Region r is nslices[r] equal slices of slice_words[r] dwords; slice s is
+// what workgroup s of the consuming launch reads, and workgroup s of a launch runs on XCD
+// s % 8, so slice s is touched by a spare workgroup on XCD s % 8. Loads only.
+constexpr int PF_REGIONS = 4;
+struct L2Prefetch {
+  int work_grid, workgroups, n;
+  const unsigned* base[PF_REGIONS];
+  int slice_words[PF_REGIONS], nslices[PF_REGIONS];
+};
+
+__device__ __forceinline__ void prefetch_slices(const L2Prefetch& a) {
+  const int p = blockIdx.x, x = p & 7, t = threadIdx.x;
+  const int k0 = (x - a.work_grid % 8 + 8) % 8;          // first spare workgroup on XCD x
+  if (a.workgroups <= k0) return;
+  const int j = (p - a.work_grid - k0) / 8;             // its index there ...
+  const int per_xcd = (a.workgroups - k0 + 7) / 8;      // ... and their number
+  unsigned acc = 0;
+#pragma unroll
+  for (int r = 0; r < PF_REGIONS; ++r) {  // constant indices: the argument arrays stay in SGPRs
+    if (r >= a.n) break;
+    const int lines = a.slice_words[r] / 32;
+    const int items = (a.nslices[r] - x + 7) / 8 * lines;
+    const unsigned* base = a.base[r];
+    for (int it = j * (int)blockDim.x + t; it < items; it += per_xcd * (int)blockDim.x) {
+      const int sl = x + 8 * (it / lines), l = it - (it / lines) * lines;
+      acc += base[(size_t)sl * a.slice_words[r] + l * 32];
+    }
+  }
+  asm volatile("" ::"v"(acc));
+}
+
+// Host side: fill `pf` from up to PF_REGIONS (pointer, bytes, slices) triples; null
+// pointers are skipped. Returns false for a region that is not whole 128-byte lines per
+// slice or not 4-byte aligned.
+inline bool make_l2_prefetch(L2Prefetch& pf, int work_grid, int spare, int n,
+                             const void* const* ptr, const size_t* bytes, const int* slices) {
+  pf = L2Prefetch{};
+  pf.work_grid = work_grid;
+  for (int r = 0; r < n && r < PF_REGIONS; ++r) {
+    if (!ptr[r]) continue;
+    const size_t b = bytes[r];
+    const int ns = slices[r];
+    if (ns <= 0 || b == 0 || b % ns || (b / ns) % 128 || b / ns / 4 > (size_t)INT32_MAX ||
+        (reinterpret_cast<uintptr_t>(ptr[r]) & 3))
+      return false;
+    pf.base[pf.n] = static_cast<const unsigned*>(ptr[r]);
+    pf.slice_words[pf.n] = static_cast<int>(b / ns / 4);
+    pf.nslices[pf.n] = ns;
+    ++pf.n;
+  }
+  pf.workgroups = pf.n ? spare : 0;
+  return true;
+}
+
+// CUs of the current device (cached per device).
+inline int device_cus() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 }  // namespace pi0

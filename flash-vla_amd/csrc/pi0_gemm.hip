@@ -567,7 +567,9 @@ static int launch_rows(const GemmArgs& a, hipStream_t s) {
   const int nrb = (a.M + 15) / 16, ntiles = a.N / 16;
   const int grid = nrb * ntiles;
   const int xcd_map = ntiles % 8 == 0;
-  // 8 waves split K (at most 16 fragments of W in registers per wave)
+  // 8 waves split K (at most 16 fragments of W in registers per wave). (Spare workgroups
+  // prefetching the ffn-down weights from this launch measured slower: it is bound by its
+  // CUs' load path.)
   switch (a.K) {
     case 512: rows16_kernel<EPI, 2, 8><<<grid, 512, 0, s>>>(a, nrb, xcd_map); break;
     case 1024: rows16_kernel<EPI, 4, 8><<<grid, 512, 0, s>>>(a, nrb, xcd_map); break;

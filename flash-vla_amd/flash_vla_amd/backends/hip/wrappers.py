@@ -343,10 +343,6 @@ def decoder_attention(Q, K, V, scores, out, encoder_seq_len):
     return out
 
 
-# regions the attention launch prefetches: the o-proj that follows it, then the FFN
-PREFETCH_OPROJ = True
-
-
 def _consumer_slices(M: int, w) -> int:
     """Slices of packed `w` such that slice s is what workgroup s of its residual GEMM reads
     (and so lands on XCD s % 8): row-split -> one column tile per slice (the tile's
@@ -355,10 +351,11 @@ def _consumer_slices(M: int, w) -> int:
     return (Nw // 16) * (1 if RESIDUAL_MODE == "rows" else _splitk(M, Nw, Kw))
 
 
-def decoder_attention_prefetch(Q, K, V, scores, out, encoder_seq_len, gate_w, up_w, down_w,
-                               o_w=None):
-    """`decoder_attention` whose spare workgroups also pull this layer's o-proj, gate / up
-    and down weights into the L2 of the XCDs that will read them (pi0hip_attention_prefetch).
+def decoder_attention_prefetch(Q, K, V, scores, out, encoder_seq_len, gate_w, up_w, down_w):
+    """`decoder_attention` whose spare workgroups also pull this layer's gate / up and
+    down weights into the L2 of the XCDs that will read them (pi0hip_attention_prefetch).
+    (Prefetching the o-proj's weights here, or the down's from spare workgroups of the
+    o-proj launch, measured slower: the o-proj is bound by its CUs' load path.)
 
     Engine-level option of this backend, not a reference call site: the reference's
     decoder_attention (fused_wrappers.py:88-115) prefetches nothing. The result is bitwise
@@ -376,13 +373,10 @@ def decoder_attention_prefetch(Q, K, V, scores, out, encoder_seq_len, gate_w, up
             or K.stride(0) != V.stride(0)):
         raise ValueError("decoder_attention: shape mismatch")
     regions = []
-    if o_w is not None and PREFETCH_OPROJ:
-        regions += [packed_weight_ptr(o_w), o_w.numel() * 2, _consumer_slices(M, o_w)]
-    else:
-        regions += [None, 0, 0]
     for w in (gate_w, up_w):
         regions += [packed_weight_ptr(w), w.numel() * 2, w.shape[1] // 16]
     regions += [packed_weight_ptr(down_w), down_w.numel() * 2, _consumer_slices(M, down_w)]
+    regions += [None, 0, 0]
     lib = _abi.lib()
     nbytes = lib.pi0hip_attention_batched_workspace_bytes(rows, keys, 1)
     ws = scratch("attn_ws", (nbytes,), torch.uint8, Q.device)

@@ -136,10 +136,9 @@ def transformer_decoder(ops, weights, buffers, encoder_seq_len, steps=10, layers
                          buffers["decoder_attn_buf"], buffers["decoder_q_buf"], encoder_seq_len)
             if attention_prefetch is None:
                 ops.decoder_attention(*attn_args)
-            else:   # same result; also pulls this layer's o-proj and FFN weights into L2
+            else:   # same result; also pulls this layer's FFN weights into L2
                 attention_prefetch(*attn_args, weights["decoder_ffn_gate_w"][i],
-                                   weights["decoder_ffn_up_w"][i], weights["decoder_ffn_down_w"][i],
-                                   weights["decoder_attn_o_w"][i])
+                                   weights["decoder_ffn_up_w"][i], weights["decoder_ffn_down_w"][i])
             ops.decoder_out_proj_residual(
                 buffers["decoder_q_buf"].view(buffers["decoder_x"].shape[0], -1), weights["decoder_attn_o_w"][i],
                 buffers["decoder_x"])

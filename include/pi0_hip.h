@@ -162,6 +162,7 @@ int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int l
 int pi0hip_linear_residual_rows(const void* x, int ldx, const void* w_packed, void* out, int ldo,
                                 int M, int N, int K, hipStream_t s);
 
+
 /* ---- unfused decoder call sites (op_table(fused=False)) ------------------------
  * The reference's two-kernel decoder path, kept for its rounding points: the RMS
  * factor is a separate pass that stores bf16 f, and x * f is rounded to bf16 per
