@@ -39,7 +39,7 @@ def test_kblock_waits_reject_a_loose_wait(gemm_asm):
     name = "_ZN3pi018skinny_gemm_kernelILi4ELb1ELi8ELi4EEEvNS_8GemmArgsE"
     start = gemm_asm.index(name + ":")
     body = gemm_asm[start:gemm_asm.index("s_endpgm", start)]
-    first = body.index("s_waitcnt vmcnt(")
+    first = body.index("s_waitcnt vmcnt(", body.index(" lds\n"))   # first k-block wait
     loose = body[:first] + "s_waitcnt vmcnt(60)" + body[body.index(")", first) + 1:]
     assert build_lib.check_kblock_waits(gemm_asm.replace(body, loose)) == [name]
 
