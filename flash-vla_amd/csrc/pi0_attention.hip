@@ -61,12 +61,13 @@ __device__ __forceinline__ int out_row(const AttnArgs& a, int b, int lr) {
 
 // Merge of one 16-byte output piece (row, columns col..col+3) over the key chunks, in chunk
 // order: O = sum_c 2^(lse_c - max) O_c / sum_c 2^(lse_c - max).
+template <int MAXC>     // MAXC >= nchunks: the loads are unrolled MAXC deep
 __device__ __forceinline__ bf16x4 merge_piece(__amdgpu_buffer_rsrc_t pr, __amdgpu_buffer_rsrc_t lr,
                                               int nchunks, int rows_pad, int row, int col) {
-  float lse_c[MAX_CHUNKS];
-  f32x4 pv[MAX_CHUNKS];
+  float lse_c[MAXC];
+  f32x4 pv[MAXC];
 #pragma unroll
-  for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
+  for (int cc = 0; cc < MAXC; ++cc) {
     const int ci = min(cc, nchunks - 1);
     lse_c[cc] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                               lr, (ci * rows_pad + row) * 4, 0, 0));
@@ -75,14 +76,14 @@ __device__ __forceinline__ bf16x4 merge_piece(__amdgpu_buffer_rsrc_t pr, __amdgp
   }
   float lmax = NEG_BIG;
 #pragma unroll
-  for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
+  for (int cc = 0; cc < MAXC; ++cc) {
     lse_c[cc] = cc < nchunks ? lse_c[cc] : NEG_BIG;
     lmax = fmaxf(lmax, lse_c[cc]);
   }
   float wsum = 0.f;
   f32x4 o4 = zero4();
 #pragma unroll
-  for (int cc = 0; cc < MAX_CHUNKS; ++cc) {
+  for (int cc = 0; cc < MAXC; ++cc) {
     const float w = cc < nchunks ? fast_exp2(lse_c[cc] - lmax) : 0.f;
     wsum += w;
     o4 += w * pv[cc];
@@ -291,19 +292,22 @@ __global__ __launch_bounds__(NWV * 64, 2) void attn_kernel(AttnArgs a) {
   }
 }
 
-// Second pass (several chunks): global thread id merges one 16-byte piece (row id / 64,
-// columns 4 (id % 64) ..) over the chunks, in chunk order.
-constexpr int CMB_THREADS = 64;     // merge threads per workgroup (408 workgroups at config 2)
+// Second pass (several chunks): workgroup = one output row (64 threads x 16-byte pieces of
+// its 256 columns), merged over the chunks in chunk order. The row index is the block
+// index, so the buffer resources are provably uniform and live in SGPRs; the loads are
+// unrolled to the smallest of 8 / MAX_CHUNKS that covers nchunks.
+constexpr int CMB_THREADS = 64;     // one row per workgroup (408 workgroups at config 2)
+static_assert(CMB_THREADS * 4 == ATT_HD, "one row per workgroup");
+template <int MAXC>
 __global__ __launch_bounds__(CMB_THREADS) void attn_combine_kernel(AttnArgs a) {
-  const int id = blockIdx.x * CMB_THREADS + threadIdx.x;
-  const int grow = id >> 6, col = (id & 63) * 4;
-  if (grow >= a.rows * a.batch) return;
+  const int grow = blockIdx.x, col = threadIdx.x * 4;
   const int bq = grow / a.rows, row = grow - bq * a.rows;
   a.part += (size_t)bq * a.nchunks * a.rows_pad * ATT_HD;
   a.lse += (size_t)bq * a.nchunks * a.rows_pad;
-  const __amdgpu_buffer_rsrc_t pr = rows_rsrc(a.part, a.nchunks * a.rows_pad * ATT_HD * (int)sizeof(float));
-  const __amdgpu_buffer_rsrc_t lr = rows_rsrc(a.lse, a.nchunks * a.rows_pad * (int)sizeof(float));
-  const bf16x4 pk = merge_piece(pr, lr, a.nchunks, a.rows_pad, row, col);
+  const __amdgpu_buffer_rsrc_t pr =
+      rows_rsrc_sgpr(a.part, a.nchunks * a.rows_pad * ATT_HD * (int)sizeof(float));
+  const __amdgpu_buffer_rsrc_t lr = rows_rsrc_sgpr(a.lse, a.nchunks * a.rows_pad * (int)sizeof(float));
+  const bf16x4 pk = merge_piece<MAXC>(pr, lr, a.nchunks, a.rows_pad, row, col);
   *reinterpret_cast<bf16x4*>(a.out + (size_t)out_row(a, bq, row) * a.ldo + col) = pk;
 }
 
@@ -354,8 +358,11 @@ static int attention_launch(const void* q, int ldq, const void* k, const void* v
   hipLaunchKernelGGL(attn_kernel<4>, dim3(grid + a.pf.workgroups, batch), dim3(256), 0, s, a);
   if (a.nchunks > 1) {
     if (hipError_t e = hipGetLastError()) return (int)e;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((batch * rows * 64 + CMB_THREADS - 1) / CMB_THREADS),
-                       dim3(CMB_THREADS), 0, s, a);
+    if (a.nchunks <= 8)
+      hipLaunchKernelGGL(attn_combine_kernel<8>, dim3(batch * rows), dim3(CMB_THREADS), 0, s, a);
+    else
+      hipLaunchKernelGGL(attn_combine_kernel<MAX_CHUNKS>, dim3(batch * rows), dim3(CMB_THREADS), 0,
+                         s, a);
   }
   return (int)hipGetLastError();
 }

@@ -644,7 +644,7 @@ __global__ __launch_bounds__(256, 1) void enc_attn_kernel(EncAttnArgs a) {
   bf16x8* qs = reinterpret_cast<bf16x8*>(&ob[0][0][0]);    // [16 kk][64 lanes]
   {
     const __amdgpu_buffer_rsrc_t qr =
-        rows_rsrc(a.q + (size_t)q0 * a.ldq, max(min(32, a.rows - q0), 0) * a.ldq * 2);
+        rows_rsrc_sgpr(a.q + (size_t)q0 * a.ldq, max(min(32, a.rows - q0), 0) * a.ldq * 2);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int kk = wave * 4 + i;
@@ -652,7 +652,7 @@ __global__ __launch_bounds__(256, 1) void enc_attn_kernel(EncAttnArgs a) {
     }
   }
   __syncthreads();
-  const __amdgpu_buffer_rsrc_t kr = rows_rsrc(a.k, a.keys * a.ldk * 2);
+  const __amdgpu_buffer_rsrc_t kr = rows_rsrc_sgpr(a.k, a.keys * a.ldk * 2);
 
   float m_run = -1.0e30f, l_run = 0.f;
   f32x16 o[8];
