@@ -580,35 +580,47 @@ constexpr int EA_HD = 256;
 
 struct EncAttnArgs {
   const __bf16* q; int ldq;
-  const __bf16* k; int ldk;
-  const __bf16* vt; int ldvt;           // V^T [256][ldvt], keys zero-padded to a multiple of 32
+  const __bf16* kp;                     // K in fragment order (see pack_kv_kernel)
+  const __bf16* vp;                     // V^T in fragment order
+  int ldvt;                             // keys zero-padded to a multiple of 64
   __bf16* out; int ldo;
   int rows, keys;                       // per request (grid.y = requests)
   float scale_log2;
   long long kv_bstride;                 // elements between two requests' K
 };
 
-// V [keys][ldv] -> V^T [256][ldvt], zero beyond `keys` (64 x 64 tiles through LDS).
-// Inside every 16-key chunk the keys are stored in the order the P^T operand uses,
-// {0-3, 8-11, 4-7, 12-15}, so one lane's 8 keys are one 16-byte load.
-__global__ __launch_bounds__(256) void transpose_v_kernel(const __bf16* __restrict__ v, int ldv,
-                                                          __bf16* __restrict__ vt, int ldvt,
-                                                          int keys, long long v_bstride) {
+// Attention pre-pass: K and V of one request in the order enc_attn_kernel's MFMA fragments
+// read them, so every fragment load of the attention is one contiguous 1 KB per wave (from
+// row-major K / V^T each 16-byte fragment sits on its own cache line). For 32-key block b:
+//   kp[((b * 16 + kk) * 64 + l) * 8 ..]          = K[32 b + l % 32][16 kk + 8 (l / 32) ..]
+//   vp[(((b * 8 + dt) * 2 + c) * 64 + l) * 8 ..] = V^T[32 dt + l % 32][slots 32 b + 16 c + 8 (l / 32) ..]
+// where V^T's key slots follow, inside every 16-key chunk, the order the P^T operand uses,
+// {0-3, 8-11, 4-7, 12-15}. Keys past `keys` (up to ldvt, a multiple of 64) are zero.
+// One workgroup: a 64-key x 64-dim tile of K (copied) and of V (transposed through LDS).
+__global__ __launch_bounds__(256) void pack_kv_kernel(const __bf16* __restrict__ k,
+                                                      const __bf16* __restrict__ v, int ldkv,
+                                                      __bf16* __restrict__ kp, __bf16* __restrict__ vp,
+                                                      int ldvt, int keys, long long kv_bstride) {
   __shared__ __attribute__((aligned(16))) __bf16 tile[64][72];
   const int k0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
-  v += (size_t)blockIdx.z * v_bstride;
-  vt += (size_t)blockIdx.z * EA_HD * ldvt;
+  k += (size_t)blockIdx.z * kv_bstride;
+  v += (size_t)blockIdx.z * kv_bstride;
+  kp += (size_t)blockIdx.z * EA_HD * ldvt;
+  vp += (size_t)blockIdx.z * EA_HD * ldvt;
   const int t = threadIdx.x;
-  // 16-byte loads: key row kr, dims 8 c .. + 7 (keys past the end read as zeros)
+  // 16-byte loads: key row kr, dims d0 + 8 c .. + 7 (keys past the end read as zeros)
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    const int i = t + 256 * j, kr = i >> 3, c = (i & 7) * 8;
-    const bf16x8 x = k0 + kr < keys ? load8(v + (size_t)(k0 + kr) * ldv + d0 + c) : zero8();
-    *reinterpret_cast<bf16x8*>(&tile[kr][c]) = x;
+    const int i = t + 256 * j, kr = i >> 3, c = (i & 7) * 8, key = k0 + kr, d = d0 + c;
+    const bool in = key < keys;
+    const bf16x8 kx = in ? load8(k + (size_t)key * ldkv + d) : zero8();
+    const bf16x8 vx = in ? load8(v + (size_t)key * ldkv + d) : zero8();
+    const int l = ((d & 15) >> 3) * 32 + (key & 31);
+    *reinterpret_cast<bf16x8*>(kp + (((size_t)(key >> 5) * 16 + (d >> 4)) * 64 + l) * 8) = kx;
+    *reinterpret_cast<bf16x8*>(&tile[kr][c]) = vx;
   }
   __syncthreads();
-  // 16-byte stores: V^T row d0 + dr, storage slots 8 c .. + 7 (each slot's key permuted
-  // into the P^T order of the attention's S^T accumulator)
+  // V^T row d, storage slots s .. s + 7 (each slot's key permuted into the P^T order)
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int i = t + 256 * j, dr = i >> 3, c = (i & 7) * 8;
@@ -619,7 +631,10 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const __bf16* __restri
       const int key = (kc & ~15) + ((sl & 4) ? 8 : 0) + ((sl & 8) ? 4 : 0) + (sl & 3);
       o[q] = tile[key][dr];
     }
-    *reinterpret_cast<bf16x8*>(vt + (size_t)(d0 + dr) * ldvt + k0 + c) = o;
+    const int d = d0 + dr, sl0 = k0 + c;                       // slot of o[0]
+    const int l = ((sl0 & 15) >> 3) * 32 + (d & 31);
+    const size_t frag = ((size_t)(sl0 >> 5) * 8 + (d >> 5)) * 2 + ((sl0 & 31) >> 4);
+    *reinterpret_cast<bf16x8*>(vp + (frag * 64 + l) * 8) = o;
   }
 }
 
@@ -635,8 +650,8 @@ __global__ __launch_bounds__(256, 1) void enc_attn_kernel(EncAttnArgs a) {
     const int bq = blockIdx.y;
     a.q += (size_t)bq * a.rows * a.ldq;
     a.out += (size_t)bq * a.rows * a.ldo;
-    a.k += (size_t)bq * a.kv_bstride;
-    a.vt += (size_t)bq * EA_HD * a.ldvt;
+    a.kp += (size_t)bq * EA_HD * a.ldvt;
+    a.vp += (size_t)bq * EA_HD * a.ldvt;
   }
 
   // Q^T fragments (B operand, 16 d each; lane holds Q[q0 + r][16 kk + 8 h .. + 7]) are
@@ -652,7 +667,6 @@ __global__ __launch_bounds__(256, 1) void enc_attn_kernel(EncAttnArgs a) {
     }
   }
   __syncthreads();
-  const __amdgpu_buffer_rsrc_t kr = rows_rsrc_sgpr(a.k, a.keys * a.ldk * 2);
 
   float m_run = -1.0e30f, l_run = 0.f;
   f32x16 o[8];
@@ -668,31 +682,35 @@ __global__ __launch_bounds__(256, 1) void enc_attn_kernel(EncAttnArgs a) {
   // each load has the other phase's 16 MFMAs to land.
   bf16x8 kf[16], vf[8][2];
   auto blk = [&](int i) { return wave + 4 * min(i, mine - 1); };   // past the end: re-load
+  // fragment-ordered K / V^T: each fragment is one contiguous 1 KB wave load
   auto load_k = [&](int i) {
-    const int key0 = blk(i) * 32;
+    const __bf16* src = a.kp + ((size_t)blk(i) * 16 * 64 + lane) * 8;
 #pragma unroll
-    for (int kk = 0; kk < 16; ++kk)
-      kf[kk] = buf_load8(kr, ((key0 + r) * a.ldk + kk * 16 + h * 8) * 2);
+    for (int kk = 0; kk < 16; ++kk) kf[kk] = load8(src + kk * 64 * 8);
   };
   auto load_v = [&](int i) {
-    const int key0 = blk(i) * 32;
+    const __bf16* src = a.vp + ((size_t)blk(i) * 16 * 64 + lane) * 8;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const __bf16* row = a.vt + (size_t)(dt * 32 + r) * a.ldvt + key0 + 8 * h;
+    for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-      for (int c = 0; c < 2; ++c) vf[dt][c] = load8(row + 16 * c);
-    }
+      for (int c = 0; c < 2; ++c) vf[dt][c] = load8(src + (dt * 2 + c) * 64 * 8);
   };
   if (mine > 0) load_k(0);
   for (int i = 0; i < mine; ++i) {
     const int key0 = (wave + 4 * i) * 32;
     load_v(i);
+    bf16x8 qv[16];
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) qv[kk] = qs[kk * 64 + lane];
+    __builtin_amdgcn_sched_barrier(0);     // keep the V^T and Q requests ahead of the S^T MFMAs
     f32x16 st;
 #pragma unroll
     for (int e = 0; e < 16; ++e) st[e] = 0.f;
 #pragma unroll
-    for (int kk = 0; kk < 16; ++kk) st = mfma32(kf[kk], qs[kk * 64 + lane], st);
+    for (int kk = 0; kk < 16; ++kk) st = mfma32(kf[kk], qv[kk], st);
+    __builtin_amdgcn_sched_barrier(0);
     load_k(i + 1);
+    __builtin_amdgcn_sched_barrier(0);     // and the next K requests ahead of the softmax
     // lane holds S^T[key 8 (e / 4) + 4 h + e % 4][query r]
     float sv[16], mx = -1.0e30f;
 #pragma unroll
@@ -1170,7 +1188,7 @@ static inline size_t round256_(size_t v) { return (v + 255) / 256 * 256; }
 size_t pi0hip_encoder_attention_batched_workspace_bytes(int keys, int batch) {
   if (keys <= 0 || batch <= 0) return 0;
   const size_t ldvt = (size_t)(keys + 63) / 64 * 64;
-  return round256_((size_t)batch * EA_HD * ldvt * sizeof(__bf16));
+  return 2 * round256_((size_t)batch * EA_HD * ldvt * sizeof(__bf16));   // packed K, packed V^T
 }
 
 size_t pi0hip_encoder_attention_workspace_bytes(int keys) {
@@ -1196,13 +1214,14 @@ int pi0hip_encoder_attention_batched(const void* q, int ldq, const void* k, cons
   if (!ws || ws_bytes < pi0hip_encoder_attention_batched_workspace_bytes(keys, batch))
     return PI0HIP_ERR_WORKSPACE;
   const int ldvt = (keys + 63) / 64 * 64;
-  hipLaunchKernelGGL(transpose_v_kernel, dim3(ldvt / 64, EA_HD / 64, batch), dim3(256), 0, s,
-                     (const __bf16*)v, ldkv, (__bf16*)ws, ldvt, keys, kv_bstride);
+  __bf16* kp = reinterpret_cast<__bf16*>(ws);
+  __bf16* vp = kp + round256_((size_t)batch * EA_HD * ldvt * sizeof(__bf16)) / sizeof(__bf16);
+  hipLaunchKernelGGL(pack_kv_kernel, dim3(ldvt / 64, EA_HD / 64, batch), dim3(256), 0, s,
+                     (const __bf16*)k, (const __bf16*)v, ldkv, kp, vp, ldvt, keys, kv_bstride);
   if (hipError_t e = hipGetLastError()) return (int)e;
   EncAttnArgs a = {};
   a.q = (const __bf16*)q; a.ldq = ldq;
-  a.k = (const __bf16*)k; a.ldk = ldkv;
-  a.vt = (const __bf16*)ws; a.ldvt = ldvt;
+  a.kp = kp; a.vp = vp; a.ldvt = ldvt;
   a.out = (__bf16*)out; a.ldo = ldo;
   a.rows = rows; a.keys = keys;
   a.scale_log2 = 1.4426950408889634f * scale;
