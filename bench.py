@@ -72,6 +72,32 @@ def _time_graph(run, n_inner, reps, torch):
     return statistics.median(samples)
 
 
+def _timed_calls(call, steps, torch):
+    """Run `call()` `steps` times on the current stream, each bracketed by its own pair of
+    HIP events, the whole region by an outer pair. Returns (median ms, timing dict)."""
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    outer = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+    torch.cuda.synchronize()
+    outer[0].record(stream)
+    for s_ev, e_ev in evs:
+        s_ev.record(stream)
+        call()
+        e_ev.record(stream)
+    outer[1].record(stream)
+    torch.cuda.synchronize()
+    samples = sorted(s_ev.elapsed_time(e_ev) for s_ev, e_ev in evs)
+    ms = statistics.median(samples)
+    ms_mean = outer[0].elapsed_time(outer[1]) / steps
+    if steps < 30:
+        print(f"[bench] note: median of {steps} calls (>= 30 recommended)", file=sys.stderr,
+              flush=True)
+    return ms, {"statistic": f"median of {steps} individually timed calls",
+                "ms_mean_bracket": round(ms_mean, 4), "ms_min": round(samples[0], 4),
+                "ms_max": round(samples[-1], 4)}
+
+
 def kernel_roofline(eng, torch):
     from flash_vla_amd.backends.hip import wrappers as W
     b, w = eng.buffers, eng.weights
@@ -179,18 +205,10 @@ def main_encoder(args, torch):
     x = encoder_inputs(seed=3).cuda()
     eng = Pi0EncoderEngine(ck, encoder_seq_len=ENC_M, copy_weights=False)
     print(f"[bench] encoder engine captured, {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
-    stream = torch.cuda.current_stream()
-    for _ in range(args.warmup):
+    for _ in range(max(args.warmup, 3)):
         eng.forward(x)
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(args.steps):
-        eng.forward(x)          # copy the [768, 2048] input into the static buffer, replay
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    # each call copies the [768, 2048] input into the static buffer and replays the graph
+    ms, timing = _timed_calls(lambda: eng.forward(x), args.steps, torch)
     flops, gate_flops = encoder_flops()
     print(f"[bench] encoder {ms:.3f} ms/encode", file=sys.stderr, flush=True)
 
@@ -224,6 +242,7 @@ def main_encoder(args, torch):
         "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
         "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
         "flops_per_encode": flops,
+        "timing": timing,
         "roofline": roof,
         "cpu_baseline": cpu,
     }
@@ -256,18 +275,10 @@ def main_full(args, torch):
     eng = Pi0Inference(ck, num_views=3, chunk_size=50, batch=B, prompt_tokens=P)
     del ck
     print(f"[bench] full forward captured, {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
-    stream = torch.cuda.current_stream()
-    for _ in range(args.warmup):
+    for _ in range(max(args.warmup, 3)):
         eng.forward(images, state, noise, ids)
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(args.steps):
-        eng.forward(images, state, noise, ids)    # copy the inputs, replay the graph
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    # each call copies the inputs into the static buffers and replays the graph
+    ms, timing = _timed_calls(lambda: eng.forward(images, state, noise, ids), args.steps, torch)
     print(f"[bench] full forward {ms:.3f} ms", file=sys.stderr, flush=True)
     config5 = B > 1 or P > 0
     M_enc = B * (768 + P)
@@ -311,7 +322,7 @@ def main_full(args, torch):
         "action_chunks_per_s": round(B * 1000.0 / ms, 2),
         "baseline_ms": None if config5 else H100_FULL_FORWARD_MS,
         "baseline_hw": None if config5 else "H100 SXM5 (published)",
-        "roofline": roof, "cpu_baseline": cpu,
+        "timing": timing, "roofline": roof, "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
 
@@ -443,25 +454,9 @@ def main():
     # events (the noise is not reset in between; each replay is a full 10-step denoise of
     # whatever the buffer holds). value = the median replay; the mean over the whole
     # bracket is reported beside it.
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
-    outer = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-    torch.cuda.synchronize()
-    outer[0].record(stream)
-    for s_ev, e_ev in evs:
-        s_ev.record(stream)
-        eng.replay()
-        e_ev.record(stream)
-    outer[1].record(stream)
-    torch.cuda.synchronize()
-    samples = sorted(s_ev.elapsed_time(e_ev) for s_ev, e_ev in evs)
-    ms = statistics.median(samples)
-    ms_mean = outer[0].elapsed_time(outer[1]) / args.steps
-    if args.steps < 30:
-        print(f"[bench] note: median of {args.steps} replays (>= 30 recommended)",
-              file=sys.stderr, flush=True)
-    print(f"[bench] {ms:.3f} ms/chunk (median of {args.steps}; bracket mean {ms_mean:.3f})",
-          file=sys.stderr, flush=True)
+    ms, timing = _timed_calls(eng.replay, args.steps, torch)
+    print(f"[bench] {ms:.3f} ms/chunk (median of {args.steps}; bracket mean "
+          f"{timing['ms_mean_bracket']:.3f})", file=sys.stderr, flush=True)
 
     roof = None if args.no_kernel else kernel_roofline(eng, torch)
     cpu = None if args.no_cpu else cpu_baseline()
@@ -481,9 +476,7 @@ def main():
         "hbm_gbs": round(gbs, 1),
         "loop_roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
         "bytes_per_chunk": CHUNK_BYTES,
-        "timing": {"statistic": f"median of {args.steps} individually timed replays",
-                   "ms_mean_bracket": round(ms_mean, 4), "ms_min": round(samples[0], 4),
-                   "ms_max": round(samples[-1], 4)},
+        "timing": timing,
         "roofline": roof,
         "cpu_baseline": cpu,
     }
