@@ -20,7 +20,9 @@ from ...arena import ScratchPool
 from . import _abi
 
 DECODER_HEADS = 8
-_TILE_M = 64            # rows of one skinny-GEMM block: beyond it the batched tile kernels run
+# Above one 64-row block (the batched decoder, M = B x 51) the decoder's GEMMs run on the
+# prefix encoder's tile kernel: the skinny kernel would stream the weights once per row block.
+_TILE_M = 64
 _POOL = ScratchPool()
 
 
@@ -392,8 +394,6 @@ def attention_prefetch_for(attention_op):
     return decoder_attention_prefetch if attention_op is decoder_attention else None
 
 
-# Above one 64-row block (the batched decoder, M = B x 51) the decoder's GEMMs run on the
-# prefix encoder's tile kernel: the skinny kernel would stream the weights once per row block.
 def _rows_ok(x, K: int, N: int) -> bool:
     """The row-split kernel's shape rules (pi0hip_linear_residual_rows)."""
     return (RESIDUAL_MODE == "rows" and x.shape[0] <= _TILE_M and K in (512, 1024, 2048, 4096)
