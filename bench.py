@@ -404,6 +404,9 @@ def main():
                     help="--workload full: prompt length in token ids (config 5: 48)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-kernel", action="store_true", help="skip the per-kernel roofline leg")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="decoder: only the gate-kernel roofline leg (no loop capture), so a "
+                         "rocprofv3 trace of this command holds just that kernel's timed launches")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy (5x), to calibrate rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE against a kernel of known traffic")
@@ -438,6 +441,11 @@ def main():
     ck = decoder_checkpoint(seed=0)
     inp = decoder_inputs(seed=1)
     print(f"[bench] inputs generated in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    if args.kernel_only:
+        eng = Pi0DecoderEngine({k: v.cuda() for k, v in ck.items()}, steps=STEPS, layers=LAYERS,
+                               capture=False)
+        print(json.dumps({"roofline": kernel_roofline(eng, torch)}), flush=True)
+        return
     eng = Pi0DecoderEngine({k: v.cuda() for k, v in ck.items()}, steps=STEPS, layers=LAYERS)
     eng.load_prefix(inp["encoder_K"].cuda(), inp["encoder_V"].cuda())
     state = inp["observation_state_normalized"].cuda()
