@@ -106,6 +106,7 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
   __shared__ bf16x8 lds[RING > PARK ? RING : PARK];
   __shared__ float rms_f[RMS ? BM : 1];
 
+  PI0_PROBE(0);
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   float ssr[FM];
 #pragma unroll
@@ -165,6 +166,7 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
 
 #pragma unroll
   for (int u = 0; u < D - 1; ++u) issue(u, u);
+  PI0_PROBE(1);
 
   for (int s0 = 0; s0 < nsteps; s0 += D) {
 #pragma unroll
@@ -172,6 +174,7 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
       const int s = s0 + u;
       __builtin_amdgcn_s_waitcnt(PI0_VMCNT(AWAIT));
       __builtin_amdgcn_s_barrier();
+      PI0_PROBE(8 + s);
       issue(s + D - 1, (u + D - 1) % D);
       // A fragments through a PF-deep register ring (f = kq * FM + i): the read of
       // fragment f + PF - 1 is issued before the MFMAs of fragment f.
@@ -204,6 +207,7 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
       }
     }
   }
+  PI0_PROBE(2);
   __builtin_amdgcn_s_waitcnt(PI0_VMCNT(0));   // drain the dummy tail loads before exit
   if constexpr (RMS) {
 #pragma unroll
@@ -309,6 +313,7 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
     for (int q = 0; q < 8; ++q) o[q] = f2bf(v[q]);
     *reinterpret_cast<bf16x8*>(dst) = o;
   }
+  PI0_PROBE(3);
 }
 
 // ---- gated FFN on a wave grid, both operands staged in LDS ---------------------------
