@@ -143,6 +143,12 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
     }
   }
 
+  // the epilogue's bias / residual pieces (8 columns of a row per thread and pass) do not
+  // depend on the product: their loads go out first and land while the k loop runs
+  constexpr int C8 = OUTC / 8, NEP = (BM * C8 + 255) / 256;
+  constexpr bool EB = EPI == TE_BIAS || EPI == TE_BIAS_RES || EPI == TE_BIAS_GELU;
+  constexpr bool ER = EPI == TE_RES || EPI == TE_BIAS_RES;
+  bf16x8 epb[EB ? NEP : 1], epr[ER ? NEP : 1];
   bf16x8 breg[D][FN][4];
   auto issue = [&](int s, int slot) {
     const int st = min(s, nsteps - 1) + step0;   // past the end: a harmless re-load
@@ -166,6 +172,28 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
 
 #pragma unroll
   for (int u = 0; u < D - 1; ++u) issue(u, u);
+  if constexpr (EB || ER) {
+    // unconditional loads through bounded resources (pieces past the end read as zeros and
+    // are never stored), so no divergent branch makes the compiler wait on the ring above
+    const __amdgpu_buffer_rsrc_t br = rows_rsrc_sgpr(a.bias, EB ? a.n_valid * (int)sizeof(__bf16) : 0);
+    const int rrows = EPI == TE_RES ? a.M : (a.res_mod ? a.res_mod : a.M);
+    const int rld = EPI == TE_RES ? a.ldo : a.ldres;
+    const __amdgpu_buffer_rsrc_t rr =
+        rows_rsrc_sgpr(EPI == TE_RES ? (const void*)a.out : (const void*)a.res,
+                       ER ? rrows * rld * (int)sizeof(__bf16) : 0);
+#pragma unroll
+    for (int k = 0; k < NEP; ++k) {
+      const int idx = t + 256 * k, row = idx / C8, c = (idx - row * C8) * 8;
+      const int grow = m0 + row, col = ntile * OUTC + c;
+      const bool in = idx < BM * C8;
+      if constexpr (EB) epb[k] = buf_load8(br, in ? col * (int)sizeof(__bf16) : INT_MAX - 64);
+      if constexpr (ER) {
+        const int rrow = EPI == TE_BIAS_RES && a.res_mod ? grow % a.res_mod : grow;
+        epr[k] = buf_load8(rr, in && rrow < rrows ? (rrow * rld + col) * (int)sizeof(__bf16) : INT_MAX - 64);
+      }
+    }
+  }
+
   PI0_PROBE(1);
 
   for (int s0 = 0; s0 < nsteps; s0 += D) {
@@ -244,8 +272,10 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
       }
   }
   __syncthreads();
-  constexpr int C8 = OUTC / 8;
-  for (int idx = t; idx < BM * C8; idx += 256) {
+#pragma unroll
+  for (int k = 0; k < NEP; ++k) {
+    const int idx = t + 256 * k;
+    if (idx >= BM * C8) continue;
     const int row = idx / C8, c = (idx - row * C8) * 8;
     const int grow = m0 + row;
     if (grow >= a.M) continue;
@@ -283,25 +313,20 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
     } else {
       dst = a.out + (size_t)grow * a.ldo + col;
       if constexpr (EPI == TE_BIAS) {
-        const bf16x8 b = load8(a.bias + col);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) v[q] += bf2f(b[q]);
+        for (int q = 0; q < 8; ++q) v[q] += bf2f(epb[k][q]);
       }
       if constexpr (EPI == TE_RES) {
-        const bf16x8 rv = load8(dst);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) v[q] += bf2f(rv[q]);
+        for (int q = 0; q < 8; ++q) v[q] += bf2f(epr[k][q]);
       }
       if constexpr (EPI == TE_BIAS_RES || EPI == TE_BIAS_GELU) {
-        const bf16x8 b = load8(a.bias + col);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) v[q] += bf2f(b[q]);
+        for (int q = 0; q < 8; ++q) v[q] += bf2f(epb[k][q]);
       }
       if constexpr (EPI == TE_BIAS_RES) {
-        const int rrow = a.res_mod ? grow % a.res_mod : grow;
-        const bf16x8 rv = load8(a.res + (size_t)rrow * a.ldres + col);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) v[q] += bf2f(rv[q]);
+        for (int q = 0; q < 8; ++q) v[q] += bf2f(epr[k][q]);
       }
       if constexpr (EPI == TE_BIAS_GELU) {
 #pragma unroll
