@@ -68,10 +68,36 @@ __host__ __device__ inline size_t part_floats(int tiles, int splitk, int nd) {
 // Epilogue of one 4-column piece of output row `row` (columns nt*16 + c4 ..+3) from
 // the fp32 accumulators v0 (and v1 for the dual gate/up GEMM) and, for the RMS
 // call sites, the row's sum of squares over the full K.
+// RoPE position of output row `row` (EPI_QKV_ROPE). Row order of a batch of B requests:
+// the B state tokens first, then the B x T action tokens request by request (for B = 1:
+// state, actions). Token t of request b takes RoPE position t, Q row b (T + 1) + t
+// (request-major) and cache row t of request b.
+__device__ __forceinline__ void qkv_token(const GemmArgs& a, int row, int& b, int& t) {
+  const int T = a.M / a.batch - 1;
+  b = 0; t = row;
+  if (a.batch > 1) {
+    if (row < a.batch) { b = row; t = 0; }
+    else { b = (row - a.batch) / T; t = 1 + (row - a.batch) - b * T; }
+  }
+}
+
+// EPI_QKV_ROPE: the (cos, sin) pairs of one 4-column piece, read before the product is
+// known (the caller issues this ahead of its operand loads). Unconditional: a resource
+// bounded to the table makes rows past M and the V columns read zeros (never used).
+__device__ __forceinline__ bf16x4 qkv_rope_piece(const GemmArgs& a, int row, int nt, int c4) {
+  const int hd = a.head_dim, qdim = a.heads * hd, n = nt * 16 + c4;
+  int b, t;
+  qkv_token(a, row, b, t);
+  const int npos = a.M / a.batch;
+  const __amdgpu_buffer_rsrc_t rr = rows_rsrc_sgpr(a.rope, npos * hd * (int)sizeof(__bf16));
+  const int off = row < a.M && n < qdim + hd ? (t * hd + n % hd) * (int)sizeof(__bf16) : INT_MAX - 64;
+  return __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(rr, off, 0, 0));
+}
+
 template <int EPI, bool DUAL>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int row, int nt, int c4,
                                               bool nf_writer, const float* v0, const float* v1,
-                                              float ss) {
+                                              float ss, bf16x4 rope4 = {}) {
   constexpr bool RMS = uses_rms(EPI);
   if (row >= a.M) return;
   const int n = nt * 16 + c4;
@@ -103,27 +129,20 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int row, int nt
 #pragma unroll
     for (int c = 0; c < 4; ++c) o[c] = gelu_tanh(v0[c] * f) * (v1[c] * f);
   } else if constexpr (EPI == EPI_QKV_ROPE) {
-    // Row order of a batch of B requests: the B state tokens first, then the B x T action
-    // tokens request by request (for B = 1: state, actions). Token t of request b takes
-    // RoPE position t, Q row b (T + 1) + t (request-major) and cache row t of request b.
     const int hd = a.head_dim, qdim = a.heads * hd;
     const int T = a.M / a.batch - 1;
-    int b = 0, t = row;
-    if (a.batch > 1) {
-      if (row < a.batch) { b = row; t = 0; }
-      else { b = (row - a.batch) / T; t = 1 + (row - a.batch) - b * T; }
-    }
+    int b, t;
+    qkv_token(a, row, b, t);
 #pragma unroll
     for (int c = 0; c < 4; ++c) o[c] = v0[c] * f;
     if (n < qdim + hd) {
-      const int rj = n % hd;
-      const __bf16* rp = a.rope + (size_t)t * hd + rj;
 #pragma unroll
       for (int p = 0; p < 4; p += 2) {
-        const float cs = bf2f(rp[p]), sn = bf2f(rp[p + 1]);
+        const float cs = bf2f(rope4[p]), sn = bf2f(rope4[p + 1]);
         const float x0 = o[p], x1 = o[p + 1];
-        o[p] = x0 * cs - x1 * sn;
-        o[p + 1] = x1 * cs + x0 * sn;
+        // explicit fused forms: the rounding does not depend on the compiler's contraction
+        o[p] = fmaf(x0, cs, -(x1 * sn));
+        o[p + 1] = fmaf(x1, cs, x0 * sn);
       }
     }
     __bf16* dst;
@@ -178,6 +197,10 @@ __global__ __launch_bounds__(NW * 64, 1) void skinny_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) fpre[mt] = bf2f(a.prescale[m0 + min(mt * 16 + (lane & 15), rows - 1)]);
   }
+  // EPI_QKV_ROPE: this thread's epilogue piece (row t / 4, columns 4 (t % 4)..) needs four
+  // RoPE table entries; issued first, they are the oldest load under every k-block wait
+  bf16x4 rope4 = {};
+  if constexpr (EPI == EPI_QKV_ROPE) rope4 = qkv_rope_piece(a, m0 + (t >> 2), nt, (t & 3) * 4);
   __builtin_amdgcn_sched_barrier(0);
   PI0_PROBE(0);
   // ---- issue: this wave's x slice [64 x KW] goes straight from L2 into LDS (buffer
@@ -306,7 +329,7 @@ __global__ __launch_bounds__(NW * 64, 1) void skinny_gemm_kernel(GemmArgs a) {
       a.ws[part_floats((int)tiles, splitk, ND) + ((size_t)tile * splitk + ks) * 64 + lrow] = ss;
     return;
   }
-  gemm_epilogue<EPI, DUAL>(a, m0 + lrow, nt, c4, (t & 3) == 0, v0, v1, ss);
+  gemm_epilogue<EPI, DUAL>(a, m0 + lrow, nt, c4, (t & 3) == 0, v0, v1, ss, rope4);
   PI0_PROBE(6);
 }
 
@@ -364,7 +387,9 @@ __global__ __launch_bounds__(RED_THREADS) void splitk_reduce_kernel(GemmArgs a) 
     *reinterpret_cast<bf16x4*>(a.out + (size_t)row * a.ldo + nt * 16 + c4) = pk;
     return;
   }
-  gemm_epilogue<EPI, DUAL>(a, row, nt, c4, (t & 3) == 0, v0, v1, ss);
+  bf16x4 rope4 = {};
+  if constexpr (EPI == EPI_QKV_ROPE) rope4 = qkv_rope_piece(a, row, nt, c4);
+  gemm_epilogue<EPI, DUAL>(a, row, nt, c4, (t & 3) == 0, v0, v1, ss, rope4);
 }
 
 // x rows are read (and copied into LDS) 16 bytes at a time; outputs are stored four
@@ -473,6 +498,17 @@ __global__ __launch_bounds__(NW * 64, 1) void rows16_kernel(GemmArgs a, int nrb,
   bf16x8 bv[KTW];
 #pragma unroll
   for (int i = 0; i < KTW; ++i) bv[i] = load8(wq + i * 512);
+  // EPI_RES: the residual element this thread finishes (row t / 16, column t % 16) does not
+  // depend on the product, so it is read now, under the same wait as the operands (an
+  // unconditional load through a resource bounded to the row block: out of range reads 0)
+  float resv = 0.f;
+  if constexpr (EPI == EPI_RES) {
+    const __amdgpu_buffer_rsrc_t orr =
+        rows_rsrc_sgpr(a.out + (size_t)m0 * a.ldo, rows * a.ldo * (int)sizeof(__bf16));
+    const int off = t < 256 ? ((t >> 4) * a.ldo + nt * 16 + (t & 15)) * (int)sizeof(__bf16)
+                            : INT_MAX - 64;
+    resv = bf2f(__builtin_bit_cast(__bf16, __builtin_amdgcn_raw_buffer_load_b16(orr, off, 0, 0)));
+  }
   __builtin_amdgcn_s_waitcnt(PI0_VMCNT(0));    // this wave's LDS copies and fragments
   __builtin_amdgcn_sched_barrier(0);
   f32x4 acc = zero4();
@@ -514,7 +550,7 @@ __global__ __launch_bounds__(NW * 64, 1) void rows16_kernel(GemmArgs a, int nrb,
   const int n = nt * 16 + col;
   const size_t o = (size_t)(m0 + row) * a.ldo + n;
   if constexpr (EPI == EPI_RES) {
-    a.out[o] = f2bf(v + bf2f(a.out[o]));
+    a.out[o] = f2bf(v + resv);
   } else if constexpr (EPI == EPI_BIAS) {
     a.out[o] = f2bf(v + bf2f(a.bias[n]));
   } else {
