@@ -65,9 +65,6 @@ __host__ __device__ inline size_t part_floats(int tiles, int splitk, int nd) {
   return (size_t)tiles * splitk * 64 * 16 * nd;
 }
 
-// Epilogue of one 4-column piece of output row `row` (columns nt*16 + c4 ..+3) from
-// the fp32 accumulators v0 (and v1 for the dual gate/up GEMM) and, for the RMS
-// call sites, the row's sum of squares over the full K.
 // RoPE position of output row `row` (EPI_QKV_ROPE). Row order of a batch of B requests:
 // the B state tokens first, then the B x T action tokens request by request (for B = 1:
 // state, actions). Token t of request b takes RoPE position t, Q row b (T + 1) + t
@@ -94,6 +91,10 @@ __device__ __forceinline__ bf16x4 qkv_rope_piece(const GemmArgs& a, int row, int
   return __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(rr, off, 0, 0));
 }
 
+// Epilogue of one 4-column piece of output row `row` (columns nt*16 + c4 ..+3) from
+// the fp32 accumulators v0 (and v1 for the dual gate/up GEMM) and, for the RMS
+// call sites, the row's sum of squares over the full K; rope4 holds the piece's RoPE
+// table entries (EPI_QKV_ROPE, read early by the caller).
 template <int EPI, bool DUAL>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int row, int nt, int c4,
                                               bool nf_writer, const float* v0, const float* v1,
