@@ -144,7 +144,8 @@ __global__ __launch_bounds__(256, OCC) void tile_gemm_kernel(TileArgs a) {
   }
 
   // the epilogue's bias / residual pieces (8 columns of a row per thread and pass) do not
-  // depend on the product: their loads go out first and land while the k loop runs
+  // depend on the product: they are loaded right after the ring's first steps are issued
+  // and land while the k loop runs
   constexpr int C8 = OUTC / 8, NEP = (BM * C8 + 255) / 256;
   constexpr bool EB = EPI == TE_BIAS || EPI == TE_BIAS_RES || EPI == TE_BIAS_GELU;
   constexpr bool ER = EPI == TE_RES || EPI == TE_BIAS_RES;
