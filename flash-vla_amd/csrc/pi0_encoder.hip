@@ -670,10 +670,11 @@ __global__ __launch_bounds__(256) void pack_kv_kernel(const __bf16* __restrict__
 }
 
 __global__ __launch_bounds__(256, 1) void enc_attn_kernel(EncAttnArgs a) {
-  constexpr int OP = 33;                               // fp32 pitch of the parked O^T columns
-  __shared__ float ob[3][EA_HD][OP];                   // waves 1..3: O^T[d][q]; first Q^T
+  constexpr int DP = EA_HD + 4;                        // fp32 pitch of a parked O row
+  __shared__ __attribute__((aligned(16))) float ob[4][32][DP];   // per wave: O[q][d]; first Q^T
   __shared__ float ml[4][2][32];                       // per wave: m and l of each query
 
+  PI0_PROBE(0);
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int r = lane & 31, h = lane >> 5;
   const int q0 = blockIdx.x * 32;
@@ -684,27 +685,6 @@ __global__ __launch_bounds__(256, 1) void enc_attn_kernel(EncAttnArgs a) {
     a.kp += (size_t)bq * EA_HD * a.ldvt;
     a.vp += (size_t)bq * EA_HD * a.ldvt;
   }
-
-  // Q^T fragments (B operand, 16 d each; lane holds Q[q0 + r][16 kk + 8 h .. + 7]) are
-  // shared by the 4 waves: staged once in LDS (in the merge buffer's space)
-  bf16x8* qs = reinterpret_cast<bf16x8*>(&ob[0][0][0]);    // [16 kk][64 lanes]
-  {
-    const __amdgpu_buffer_rsrc_t qr =
-        rows_rsrc_sgpr(a.q + (size_t)q0 * a.ldq, max(min(32, a.rows - q0), 0) * a.ldq * 2);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int kk = wave * 4 + i;
-      qs[kk * 64 + lane] = buf_load8(qr, (r * a.ldq + kk * 16 + h * 8) * 2);
-    }
-  }
-  __syncthreads();
-
-  float m_run = -1.0e30f, l_run = 0.f;
-  f32x16 o[8];
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
 
   const int nblk = (a.keys + 31) / 32;
   const int mine = nblk > wave ? (nblk - wave + 3) / 4 : 0;     // blocks b = wave + 4 i
@@ -726,9 +706,33 @@ __global__ __launch_bounds__(256, 1) void enc_attn_kernel(EncAttnArgs a) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) vf[dt][c] = load8(src + (dt * 2 + c) * 64 * 8);
   };
-  if (mine > 0) load_k(0);
+  if (mine > 0) load_k(0);                  // block 0's K is in flight during the Q staging
+
+  // Q^T fragments (B operand, 16 d each; lane holds Q[q0 + r][16 kk + 8 h .. + 7]) are
+  // shared by the 4 waves: staged once in LDS (in the merge buffer's space)
+  bf16x8* qs = reinterpret_cast<bf16x8*>(&ob[0][0][0]);    // [16 kk][64 lanes]
+  {
+    const __amdgpu_buffer_rsrc_t qr =
+        rows_rsrc_sgpr(a.q + (size_t)q0 * a.ldq, max(min(32, a.rows - q0), 0) * a.ldq * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kk = wave * 4 + i;
+      qs[kk * 64 + lane] = buf_load8(qr, (r * a.ldq + kk * 16 + h * 8) * 2);
+    }
+  }
+  __syncthreads();
+  PI0_PROBE(1);
+
+  float m_run = -1.0e30f, l_run = 0.f;
+  f32x16 o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+
   for (int i = 0; i < mine; ++i) {
     const int key0 = (wave + 4 * i) * 32;
+    PI0_PROBE(8 + i);
     load_v(i);
     bf16x8 qv[16];
 #pragma unroll
@@ -772,19 +776,21 @@ __global__ __launch_bounds__(256, 1) void enc_attn_kernel(EncAttnArgs a) {
       o[dt] = acc;
     }
   }
+  PI0_PROBE(2);
   __syncthreads();                                     // every wave is done with qs
 
-  // ---- merge the 4 waves' partials: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w
+  // ---- merge the 4 waves' partials: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w.
+  // Every wave parks its O rows (lane: query r, 4 consecutive d per 16-byte store), then
+  // wave w finishes head dims 64 w .. 64 w + 63 of all 32 rows, summing the waves in order.
   if (h == 0) { ml[wave][0][r] = m_run; ml[wave][1][r] = l_run; }
-  if (wave > 0) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
+  for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        ob[wave - 1][dt * 32 + 8 * (e >> 2) + 4 * h + (e & 3)][r] = o[dt][e];
-  }
+    for (int e4 = 0; e4 < 4; ++e4) {
+      const f32x4 v4 = {o[dt][e4 * 4], o[dt][e4 * 4 + 1], o[dt][e4 * 4 + 2], o[dt][e4 * 4 + 3]};
+      *reinterpret_cast<f32x4*>(&ob[wave][r][dt * 32 + 8 * e4 + 4 * h]) = v4;
+    }
   __syncthreads();
-  if (wave > 0) return;
   float M = -1.0e30f;
 #pragma unroll
   for (int w = 0; w < 4; ++w) M = fmaxf(M, ml[w][0][r]);
@@ -799,20 +805,17 @@ __global__ __launch_bounds__(256, 1) void enc_attn_kernel(EncAttnArgs a) {
   if (row >= a.rows) return;
   __bf16* orow = a.out + (size_t)row * a.ldo;
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int e4 = 0; e4 < 4; ++e4) {           // 4 consecutive d per store
-      bf16x4 pk;
+    for (int e4 = 0; e4 < 4; ++e4) {           // 4 consecutive d per load and store
+      const int d0 = (2 * wave + j) * 32 + 8 * e4 + 4 * h;
+      f32x4 v = *reinterpret_cast<const f32x4*>(&ob[0][r][d0]) * wgt[0];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int d = dt * 32 + 8 * e4 + 4 * h + e;
-        float v = o[dt][e4 * 4 + e] * wgt[0];
-#pragma unroll
-        for (int w = 1; w < 4; ++w) v += ob[w - 1][d][r] * wgt[w];
-        pk[e] = f2bf(v * inv);
-      }
-      *reinterpret_cast<bf16x4*>(orow + dt * 32 + 8 * e4 + 4 * h) = pk;
+      for (int w = 1; w < 4; ++w) v += *reinterpret_cast<const f32x4*>(&ob[w][r][d0]) * wgt[w];
+      const bf16x4 pk = {f2bf(v[0] * inv), f2bf(v[1] * inv), f2bf(v[2] * inv), f2bf(v[3] * inv)};
+      *reinterpret_cast<bf16x4*>(orow + d0) = pk;
     }
+  PI0_PROBE(3);
 }
 
 
