@@ -891,6 +891,7 @@ struct VisAttnArgs {
 };
 
 __global__ __launch_bounds__(64, 1) void vision_attn_kernel(VisAttnArgs a) {
+  PI0_PROBE(0);
   const int lane = threadIdx.x, r = lane & 31, h = lane >> 5;
   const int qt = blockIdx.x, head = blockIdx.y, view = blockIdx.z;
   const size_t row0 = (size_t)view * VA_TOK;
@@ -931,6 +932,7 @@ __global__ __launch_bounds__(64, 1) void vision_attn_kernel(VisAttnArgs a) {
 #pragma unroll
   for (int kb = 0; kb < NB; ++kb) {
     const int sl = kb % RS;
+    PI0_PROBE(8 + kb);
     f32x16 st;
 #pragma unroll
     for (int e = 0; e < 16; ++e) st[e] = 0.f;
@@ -963,6 +965,7 @@ __global__ __launch_bounds__(64, 1) void vision_attn_kernel(VisAttnArgs a) {
     if (kb + RS < NB) load_blk(kb + RS);
     __builtin_amdgcn_sched_barrier(0);                 // keep each refill in its iteration
   }
+  PI0_PROBE(2);
   // lane holds O^T[d = 32 dt + 8 (e / 4) + 4 h + e % 4][query r]
   const float inv = __builtin_amdgcn_rcpf(l_run);
   __bf16* orow = a.out + (row0 + q) * a.ldo + head * VA_HD;
@@ -977,6 +980,7 @@ __global__ __launch_bounds__(64, 1) void vision_attn_kernel(VisAttnArgs a) {
         *reinterpret_cast<bf16x4*>(orow + d) = pk;
       }
     }
+  PI0_PROBE(3);
 }
 
 
