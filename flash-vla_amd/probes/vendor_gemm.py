@@ -1,6 +1,7 @@
 """Measurement probe (not part of the library): this library's tile GEMMs against the vendor
 GEMM that torch.mm / torch.addmm dispatch to on ROCm (hipBLASLt / rocBLAS), at the prefix
-encoder's and the vision tower's shapes. Each call site is captured 4 x 18 times in one
+encoder's and the vision tower's shapes (M = 768) and at the decoder's (M = 51, through the
+backend's call-site wrappers, fused epilogues included). Each call site is captured 4 x 18 times in one
 hipGraph, cycling 18 weight matrices (so the weights stream from HBM as in the model), and the
 median over 20 replays is printed per call.
 
@@ -124,6 +125,33 @@ def main():
                     out.data_ptr(), N, M, N, K, N_pad, K_pad, W._stream()))
                 vendor = time_graph(lambda i: torch.mm(x[:, :K], ws_t[i % LAYERS], out=out))
             row(name, M, K, N, ours, vendor)
+        # decoder call sites at M = 51 (config 2): ours fused (RMS factor, RoPE, GeGLU, residual)
+        M = 51
+        x = (torch.randn(M, 1024, device="cuda")).to(torch.bfloat16)
+        wq = weights(1024, 2560)
+        rope = torch.ones(M, 256, device="cuda", dtype=torch.bfloat16)
+        q = torch.empty(M * 8, 256, device="cuda", dtype=torch.bfloat16)
+        kc = torch.empty(M, 256, device="cuda", dtype=torch.bfloat16)
+        vc = torch.empty(M, 256, device="cuda", dtype=torch.bfloat16)
+        nf = torch.empty(M, device="cuda", dtype=torch.bfloat16)
+        outq = torch.empty(M, 2560, device="cuda", dtype=torch.bfloat16)
+        ours = time_graph(lambda i: W.decoder_norm_qkv_rope(x, wq[i % LAYERS], rope, q, kc, vc, nf))
+        vendor = time_graph(lambda i: torch.mm(x, wq[i % LAYERS], out=outq))
+        row("decoder norm + QKV + RoPE", M, 1024, 2560, ours, vendor)
+        wg, wu = weights(1024, 4096), weights(1024, 4096)
+        wcat = [torch.cat([g, u], dim=1) for g, u in zip(wg, wu)]
+        hid = torch.empty(M, 4096, device="cuda", dtype=torch.bfloat16)
+        hid2 = torch.empty(M, 8192, device="cuda", dtype=torch.bfloat16)
+        ours = time_graph(lambda i: W.decoder_norm_gated_ffn(x, wg[i % LAYERS], wu[i % LAYERS], hid, None))
+        vendor = time_graph(lambda i: torch.mm(x, wcat[i % LAYERS], out=hid2))
+        row("decoder norm + gate / up + GeGLU", M, 1024, 8192, ours, vendor)
+        for name, K in (("decoder o-proj + residual", 2048), ("decoder ffn-down + residual", 4096)):
+            xa = (torch.randn(M, K, device="cuda")).to(torch.bfloat16)
+            wr = weights(K, 1024)
+            res = torch.randn(M, 1024, device="cuda").to(torch.bfloat16)
+            ours = time_graph(lambda i: W.decoder_out_proj_residual(xa, wr[i % LAYERS], res))
+            vendor = time_graph(lambda i: torch.addmm(res, xa, wr[i % LAYERS], out=res))
+            row(name, M, K, 1024, ours, vendor)
 
 
 if __name__ == "__main__":
