@@ -152,6 +152,30 @@ def main():
             ours = time_graph(lambda i: W.decoder_out_proj_residual(xa, wr[i % LAYERS], res))
             vendor = time_graph(lambda i: torch.addmm(res, xa, wr[i % LAYERS], out=res))
             row(name, M, K, 1024, ours, vendor)
+        # attention against torch's scaled_dot_product_attention (one KV head, expanded)
+        import flash_vla_amd.backends.hip.encoder_wrappers as EW
+        F = torch.nn.functional
+        print("\n| attention | shape | ours us | vendor us |\n|---|---|---:|---:|")
+        q = (torch.randn(408, 256, device="cuda")).to(torch.bfloat16)
+        k = (torch.randn(819, 256, device="cuda")).to(torch.bfloat16)
+        v = (torch.randn(819, 256, device="cuda")).to(torch.bfloat16)
+        o = torch.empty_like(q)
+        mask = torch.ones(408, 819, dtype=torch.bool, device="cuda")
+        mask[:8, 769:] = False                         # the state token's rows see the prefix + itself
+        q4 = q.view(51, 8, 256).transpose(0, 1).unsqueeze(0)
+        k4, v4 = k.view(1, 1, 819, 256).expand(1, 8, 819, 256), v.view(1, 1, 819, 256).expand(1, 8, 819, 256)
+        m4 = mask.view(51, 8, 819).transpose(0, 1).unsqueeze(0)
+        ours = time_graph(lambda i: W.decoder_attention(q, k, v, None, o, 768))
+        vendor = time_graph(lambda i: F.scaled_dot_product_attention(q4, k4, v4, attn_mask=m4))
+        print(f"| decoder (merge launch included, no prefetch) | 51 tokens x 8 heads, 819 keys | {ours:.1f} | {vendor:.1f} |")
+        q = (torch.randn(6144, 256, device="cuda")).to(torch.bfloat16)
+        k = (torch.randn(768, 256, device="cuda")).to(torch.bfloat16)
+        v = (torch.randn(768, 256, device="cuda")).to(torch.bfloat16)
+        q4 = q.view(768, 8, 256).transpose(0, 1).unsqueeze(0)
+        k4, v4 = k.view(1, 1, 768, 256).expand(1, 8, 768, 256), v.view(1, 1, 768, 256).expand(1, 8, 768, 256)
+        ours = time_graph(lambda i: EW.encoder_attention(q, k, v, 256 ** -0.5))
+        vendor = time_graph(lambda i: F.scaled_dot_product_attention(q4, k4, v4))
+        print(f"| encoder (K / V fragment pre-pass included) | 768 tokens x 8 heads, 768 keys | {ours:.1f} | {vendor:.1f} |")
 
 
 if __name__ == "__main__":
