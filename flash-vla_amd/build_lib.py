@@ -47,8 +47,9 @@ def check_kblock_waits(asm: str) -> list[str]:
     """Names of skinny GEMM kernels whose k-block waits do not cover their LDS copies.
 
     skinny_gemm_kernel issues, per k-block, buffer loads that write x straight into
-    LDS and then that k-block's weight loads; before the MFMAs of k-block j it waits
-    with vmcnt(N). Vector-memory operations complete in issue order, so the wait is
+    LDS and that k-block's weight loads (x first, or the weights some k-blocks ahead:
+    one k-block's copies are contiguous, the k-blocks' copies go out in order, and the
+    loop waits once per k-block); before the MFMAs of k-block j it waits with vmcnt(N). Vector-memory operations complete in issue order, so the wait is
     sufficient only if N is at most the number of operations issued after k-block j's
     last LDS copy. This re-checks that order in the generated code (the scheduling
     barriers in the source are what keep it).
@@ -61,10 +62,15 @@ def check_kblock_waits(asm: str) -> list[str]:
         issue = [i for i, ln in enumerate(lines[:first_ds])
                  if ln.startswith(("global_load", "buffer_load"))]
         kinds = ["lds" if lines[i].endswith(" lds") else "reg" for i in issue]
-        last_copy = [j for j, k in enumerate(kinds)
-                     if k == "lds" and (j + 1 == len(kinds) or kinds[j + 1] != "lds")]
         waits = [int(w) for w in re.findall(r"s_waitcnt vmcnt\((\d+)\)",
                                             "\n".join(lines[issue[-1] + 1:]))]
+        tail = lines[issue[-1] + 1:]
+        loop = "\n".join(tail[:next((i for i, ln in enumerate(tail) if ln.startswith("s_barrier")),
+                                     len(tail))])
+        nkb = len(re.findall(r"s_waitcnt vmcnt\(\d+\)", loop))
+        copies = [j for j, k in enumerate(kinds) if k == "lds"]
+        per = len(copies) // nkb if nkb and len(copies) % nkb == 0 else 0
+        last_copy = copies[per - 1::per] if per else []
         ok = bool(last_copy) and len(waits) >= len(last_copy) and all(
             waits[j] <= len(kinds) - 1 - c for j, c in enumerate(last_copy))
         if not ok:

@@ -160,7 +160,26 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int row, int nt
   *reinterpret_cast<bf16x4*>(a.out + (size_t)row * a.ldo + n) = pk;
 }
 
-template <int EPI, bool DUAL, int KTW, int NW>
+// Issue sequence of the staging loads: with WL < 0 each k-block's x rows then its
+// weights; with WL >= 0 the weights of k-block s, then the x rows of k-block s - WL.
+// ops_after(kb) = vector-memory ops issued after both halves of k-block kb.
+template <int NKB, int WL, int XOPS, int WOPS>
+constexpr int ops_after(int kb) {
+  int pos = 0, done_x = -1, done_w = -1;
+  const int steps = WL < 0 ? NKB : NKB + WL;
+  for (int st = 0; st < steps; ++st) {
+    if (WL < 0) {
+      pos += XOPS; if (st == kb) done_x = pos;
+      pos += WOPS; if (st == kb) done_w = pos;
+    } else {
+      if (st < NKB) { pos += WOPS; if (st == kb) done_w = pos; }
+      if (st >= WL) { pos += XOPS; if (st - WL == kb) done_x = pos; }
+    }
+  }
+  return pos - (done_x > done_w ? done_x : done_w);
+}
+
+template <int EPI, bool DUAL, int KTW, int NW, int WL = -1>
 __global__ __launch_bounds__(NW * 64, 1) void skinny_gemm_kernel(GemmArgs a) {
   constexpr int ND = DUAL ? 2 : 1;
   constexpr bool RMS = uses_rms(EPI);
@@ -215,8 +234,7 @@ __global__ __launch_bounds__(NW * 64, 1) void skinny_gemm_kernel(GemmArgs a) {
     const int lrow0 = lane / BCH, lp = lane % BCH;
     const __bf16* wp = a.w0 + ((size_t)nt * KT + kt0) * 512 + lane * 8;
     const __bf16* wq = a.w1 + ((size_t)nt * KT + kt0) * 512 + lane * 8;
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
+    auto issue_x = [&](int kb) {
 #pragma unroll
       for (int q = 0; q < XIB; ++q) {
         const int row = q * BRPI + lrow0, c = lp ^ swz(row);
@@ -224,12 +242,24 @@ __global__ __launch_bounds__(NW * 64, 1) void skinny_gemm_kernel(GemmArgs a) {
                        (row * a.ldx + (kt0 + kb * KB) * 32 + c * 8) * (int)sizeof(__bf16));
       }
       __builtin_amdgcn_sched_barrier(0);
+    };
+    auto issue_w = [&](int kb) {
 #pragma unroll
       for (int k2 = 0; k2 < KB; ++k2) {
         b0[kb * KB + k2] = load8(wp + (kb * KB + k2) * 512);
         if constexpr (DUAL) b1[kb * KB + k2] = load8(wq + (kb * KB + k2) * 512);
       }
       __builtin_amdgcn_sched_barrier(0);
+    };
+    if constexpr (WL < 0) {
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) { issue_x(kb); issue_w(kb); }
+    } else {
+#pragma unroll
+      for (int st = 0; st < NKB + WL; ++st) {
+        if (st < NKB) issue_w(st);
+        if (st >= WL) issue_x(st - WL);
+      }
     }
   }
   PI0_PROBE(3);
@@ -244,14 +274,15 @@ __global__ __launch_bounds__(NW * 64, 1) void skinny_gemm_kernel(GemmArgs a) {
   for (int i = 0; i < KTW; ++i) {
     if (i % KB == 0) {
       // k-block i / KB: memory operations complete in issue order, so once at most the
-      // later k-blocks' OPS each are outstanding, its x chunks are in LDS and its
-      // weight fragments in registers
+      // operations issued after both of its halves are outstanding, its x chunks are in
+      // LDS and its weight fragments in registers
       __builtin_amdgcn_sched_barrier(0);
-      switch (NKB - 1 - i / KB) {   // folds to one s_waitcnt once the loop is unrolled
-        case 0: __builtin_amdgcn_s_waitcnt(PI0_VMCNT(0)); break;
-        case 1: __builtin_amdgcn_s_waitcnt(PI0_VMCNT(OPS)); break;
-        case 2: __builtin_amdgcn_s_waitcnt(PI0_VMCNT(2 * OPS)); break;
-        default: __builtin_amdgcn_s_waitcnt(PI0_VMCNT(3 * OPS)); break;
+      constexpr int WOPS = KB * ND;
+      switch (i / KB) {   // folds to one s_waitcnt once the loop is unrolled
+        case 0: __builtin_amdgcn_s_waitcnt(PI0_VMCNT((ops_after<NKB, WL, XIB, WOPS>(0)))); break;
+        case 1: __builtin_amdgcn_s_waitcnt(PI0_VMCNT((ops_after<NKB, WL, XIB, WOPS>(1)))); break;
+        case 2: __builtin_amdgcn_s_waitcnt(PI0_VMCNT((ops_after<NKB, WL, XIB, WOPS>(2)))); break;
+        default: __builtin_amdgcn_s_waitcnt(PI0_VMCNT((ops_after<NKB, WL, XIB, WOPS>(3)))); break;
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -421,7 +452,13 @@ static int launch_gemm(const GemmArgs& a, hipStream_t s) {
   if (ktw == 1) PI0_SKINNY(1, 4);
   else if (ktw == 2) PI0_SKINNY(2, 4);
   else if (ktw == 4) PI0_SKINNY(4, 4);
-  else if (ktw == 8) PI0_SKINNY(8, 4);
+  else if (ktw == 8) {
+    // QKV: all weight fragments before the x rows. Inside the decoder loop x comes from the
+    // previous launch's freshly written rows while the weights stream cold from HBM, so the
+    // weights go first: 0.055 ms per chunk. The gate measured 6% slower alone that way.
+    if constexpr (EPI == EPI_QKV_ROPE) skinny_gemm_kernel<EPI, DUAL, 8, 4, 4><<<grid, 256, 0, s>>>(a);
+    else PI0_SKINNY(8, 4);
+  }
   else return PI0HIP_ERR_SHAPE;
 #undef PI0_SKINNY
   if (a.splitk > 1) {

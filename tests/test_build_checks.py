@@ -35,8 +35,10 @@ def test_kblock_waits_hold(gemm_asm):
     assert build_lib.check_kblock_waits(gemm_asm) == []
 
 
-def test_kblock_waits_reject_a_loose_wait(gemm_asm):
-    name = "_ZN3pi018skinny_gemm_kernelILi4ELb1ELi8ELi4EEEvNS_8GemmArgsE"
+# the gate kernel (x rows then weights per k-block) and the QKV kernel (all weights first)
+@pytest.mark.parametrize("name", ["_ZN3pi018skinny_gemm_kernelILi4ELb1ELi8ELi4ELin1EEEvNS_8GemmArgsE",
+                                  "_ZN3pi018skinny_gemm_kernelILi3ELb0ELi8ELi4ELi4EEEvNS_8GemmArgsE"])
+def test_kblock_waits_reject_a_loose_wait(gemm_asm, name):
     start = gemm_asm.index(name + ":")
     body = gemm_asm[start:gemm_asm.index("s_endpgm", start)]
     first = body.index("s_waitcnt vmcnt(", body.index(" lds\n"))   # first k-block wait
