@@ -35,9 +35,13 @@ def test_kblock_waits_hold(gemm_asm):
     assert build_lib.check_kblock_waits(gemm_asm) == []
 
 
-# the gate kernel (x rows then weights per k-block) and the QKV kernel (all weights first)
-@pytest.mark.parametrize("name", ["_ZN3pi018skinny_gemm_kernelILi4ELb1ELi8ELi4ELin1EEEvNS_8GemmArgsE",
-                                  "_ZN3pi018skinny_gemm_kernelILi3ELb0ELi8ELi4ELi4EEEvNS_8GemmArgsE"])
+# the gate kernel (x rows then weights per k-block), the QKV kernel (all weights first),
+# each also with 56 of the 64 rows staged
+@pytest.mark.parametrize("name", [
+    "_ZN3pi018skinny_gemm_kernelILi4ELb1ELi8ELi4ELin1ELi64EEEvNS_8GemmArgsE",
+    "_ZN3pi018skinny_gemm_kernelILi4ELb1ELi8ELi4ELin1ELi56EEEvNS_8GemmArgsE",
+    "_ZN3pi018skinny_gemm_kernelILi3ELb0ELi8ELi4ELi4ELi64EEEvNS_8GemmArgsE",
+    "_ZN3pi018skinny_gemm_kernelILi3ELb0ELi8ELi4ELi4ELi56EEEvNS_8GemmArgsE"])
 def test_kblock_waits_reject_a_loose_wait(gemm_asm, name):
     start = gemm_asm.index(name + ":")
     body = gemm_asm[start:gemm_asm.index("s_endpgm", start)]

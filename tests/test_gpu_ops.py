@@ -91,7 +91,7 @@ def test_action_mlp_into_row_view():
     assert torch.all(xbuf[0] == 7.0)      # row 0 (state) untouched
 
 
-@pytest.mark.parametrize("M", [51, 1, 64, 100])
+@pytest.mark.parametrize("M", [51, 1, 56, 57, 64, 100])
 def test_norm_qkv_rope(M):
     x = rnd((M, 1024), 11)
     w = rnd((1024, 2560), 12, 0.02)
@@ -182,14 +182,29 @@ def test_residual_splitk_is_deterministic_and_reentrant(M):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
 
 
-@pytest.mark.parametrize("M", [51, 7, 204, 100])
+@pytest.mark.parametrize("M", [51, 7, 56, 57, 64, 204, 100])
 def test_norm_gated_ffn(M):
-    """M > 64 runs on the tile kernel with the RMS factor fused (f rounded to bf16)."""
+    """M > 64 runs on the tile kernel with the RMS factor fused (f rounded to bf16); up to
+    56 rows the skinny kernel stages only rows 0-55 of its 64-row block."""
     x = rnd((M, 1024), 27)
     wg, wu = rnd((1024, 4096), 28, 0.02), rnd((1024, 4096), 29, 0.02)
     out = torch.zeros(M, 4096, dtype=torch.bfloat16, device=DEV)
     W.decoder_norm_gated_ffn(x.to(DEV), wg.to(DEV), wu.to(DEV), out, None)
     close(out, O.op_norm_gated_ffn(x.float(), wg.float(), wu.float()), what=f"gated_ffn M={M}")
+
+
+def test_unstaged_rows_do_not_leak():
+    """At M <= 56 the skinny GEMMs leave LDS rows 56-63 unloaded: NaNs staged there by a
+    preceding 64-row launch (same kernels, same LDS) must not reach the 51 output rows."""
+    wg, wu = rnd((1024, 4096), 28, 0.02).to(DEV), rnd((1024, 4096), 29, 0.02).to(DEV)
+    xn = rnd((64, 1024), 30).to(DEV)
+    xn[51:] = float("nan")
+    W.decoder_norm_gated_ffn(xn, wg, wu, torch.empty(64, 4096, dtype=torch.bfloat16, device=DEV), None)
+    x = rnd((51, 1024), 27)
+    out = torch.zeros(51, 4096, dtype=torch.bfloat16, device=DEV)
+    W.decoder_norm_gated_ffn(x.to(DEV), wg, wu, out, None)
+    assert torch.isfinite(out.float()).all()
+    close(out, O.op_norm_gated_ffn(x.float(), wg.cpu().float(), wu.cpu().float()), what="gated_ffn after NaN rows")
 
 
 def test_action_out_proj_euler_update():
