@@ -1281,11 +1281,14 @@ int pi0hip_tile_linear_bias_res(const void* x, int ldx, const void* w_packed, co
   a.n_valid = N;
   a.bias = (const __bf16*)bias;
   a.res = (const __bf16*)res; a.ldres = ldres; a.res_mod = res_mod;
-  if (M >= 2048) return launch_tile_auto<128, 32, 8, TE_BIAS_RES, false>(a, s);
-  // vision o-proj (K = 1152, 18 steps): a 3-deep ring, 7.1 us against 7.8-8.0 with 6
-  if ((K_pad / 64) % 3 == 0 && (K_pad / 64) % 4 != 0)
-    return launch_tile<32, 32, 3, TE_BIAS_RES, false, 1>(a, s);
-  return launch_tile_auto<32, 32, 8, TE_BIAS_RES, false>(a, s);
+  // vision o-proj (K = 1152, 18 steps): a 3-deep ring, 7.1 us against 7.8-8.0 with 6 at
+  // M = 768, 17.3 against 19.2 at M = 3072
+  const bool d3 = (K_pad / 64) % 3 == 0 && (K_pad / 64) % 4 != 0;
+  if (M >= 2048)
+    return d3 ? launch_tile<128, 32, 3, TE_BIAS_RES, false, 1>(a, s)
+              : launch_tile_auto<128, 32, 8, TE_BIAS_RES, false>(a, s);
+  return d3 ? launch_tile<32, 32, 3, TE_BIAS_RES, false, 1>(a, s)
+            : launch_tile_auto<32, 32, 8, TE_BIAS_RES, false>(a, s);
 }
 
 int pi0hip_tile_linear_bias_gelu(const void* x, int ldx, const void* w_packed, const void* bias,

@@ -47,7 +47,7 @@ def _out_with_sentinel(M, N, ld):
     return store, store.view(M + 3, ld)
 
 
-@pytest.mark.parametrize("M", [100, 300])
+@pytest.mark.parametrize("M", [100, 300, 2100])      # 2100: the 128-row tiles used from 2048 rows
 @pytest.mark.parametrize("res_mod", [0, 256])
 def test_bias_residual_ragged(M, res_mod):
     K, N, N_pad, K_pad = 1152, 1144, 1152, 1152      # N = 1144: the last 8 packed columns padded
