@@ -41,7 +41,7 @@ CHUNK_BYTES = STEPS * STEP_BYTES           # 6,411,223,680 B
 GATE_BYTES = 2 * 1024 * 4096 * 2           # gate + up weights of one layer (activations excluded)
 # HBM bytes per launch from rocprofv3 FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0 (KiB; factors from a
 # plain 256 MiB copy); profiles/kernels_hbm_traffic_config2_config3.md
-GATE_TRAFFIC_BYTES = (8649.0 * 2.0 + 408.0 * 1.0) * 1024
+GATE_TRAFFIC_BYTES = (8645.0 * 2.0 + 408.0 * 1.0) * 1024
 ENC_GATE_TRAFFIC_BYTES = (77975.5 * 2.0 + 24576.0 * 1.0) * 1024
 
 
