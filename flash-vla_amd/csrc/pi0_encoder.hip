@@ -890,10 +890,13 @@ struct VisAttnArgs {
   float scale_log2;
 };
 
-__global__ __launch_bounds__(64, 1) void vision_attn_kernel(VisAttnArgs a) {
+// One wave per 32 queries of a (view, head); a workgroup holds NWQ consecutive query tiles
+// of the same (view, head), whose waves read the same K / V^T fragments.
+template <int NWQ>
+__global__ __launch_bounds__(64 * NWQ, 1) void vision_attn_kernel(VisAttnArgs a) {
   PI0_PROBE(0);
-  const int lane = threadIdx.x, r = lane & 31, h = lane >> 5;
-  const int qt = blockIdx.x, head = blockIdx.y, view = blockIdx.z;
+  const int lane = threadIdx.x & 63, r = lane & 31, h = lane >> 5;
+  const int qt = blockIdx.x * NWQ + (threadIdx.x >> 6), head = blockIdx.y, view = blockIdx.z;
   const size_t row0 = (size_t)view * VA_TOK;
   const int q = qt * 32 + r;
   // Q^T fragments: lane holds Q[q][16 kk + 8 h .. + 7] (zero past d = 72)
@@ -1345,7 +1348,10 @@ int pi0hip_vision_attention(const void* qkv, int ldqkv, void* out, int ldo, int 
   a.out = (__bf16*)out; a.ldo = ldo;
   a.heads = heads; a.dim = dim;
   a.scale_log2 = 1.4426950408889634f * scale;
-  hipLaunchKernelGGL(vision_attn_kernel, dim3(VA_TOK / 32, heads, views), dim3(64), 0, s, a);
+  // two 32-query tiles of one (view, head) per workgroup: their identical K / V^T fragment
+  // loads meet in one CU's L1 (3 views: 14.5 -> 13.8 us with the V^T pass, 12 views:
+  // 37.9 -> 35.8; four tiles: 17.9 / 35.3)
+  hipLaunchKernelGGL(vision_attn_kernel<2>, dim3(VA_TOK / 64, heads, views), dim3(128), 0, s, a);
   return (int)hipGetLastError();
 }
 
