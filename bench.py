@@ -112,6 +112,13 @@ def kernel_roofline(eng, torch):
             "avg_launch_us": round(us, 3), "bytes_per_launch": GATE_BYTES}
 
 
+def boundary_us(torch) -> float:
+    """Cost of one dependent dispatch in a graph: median microseconds per launch of a
+    graph of 256 chained one-element kernels (`x += 1`, no memory traffic to speak of)."""
+    x = torch.zeros(1, device="cuda")
+    return _time_graph(lambda i: x.add_(1.0), n_inner=256, reps=10, torch=torch)
+
+
 def host_threads() -> int:
     """Threads for the CPU legs: the box's CPU share (OMP_NUM_THREADS, 16 on the GPU pool),
     capped by the cores the OS reports."""
@@ -468,6 +475,11 @@ def main():
 
     roof = None if args.no_kernel else kernel_roofline(eng, torch)
     cpu = None if args.no_cpu else cpu_baseline()
+    # lower-bound model of the loop: every kernel / copy node of the captured chain is one
+    # dependent dispatch, and one dispatch costs at least an empty kernel's boundary
+    nodes = eng.graph_nodes()
+    launches = sum(v for k, v in nodes.items() if k in ("kernel", "memcpy", "memset"))
+    b_us = boundary_us(torch)
 
     gbs = CHUNK_BYTES / (ms * 1e-3) / 1e9
     out = {
@@ -479,8 +491,16 @@ def main():
         "config": {"workload": "Pi0 decoder loop, BASELINE config 2: 10 Euler steps x 18 layers, "
                                "M=51 rows (1 state + 50 actions), 8 q heads / 1 kv head x 256, "
                                "keys 819, width 1024, FFN 4096, batch 1",
-                   "global_batch": 1, "seq_len": 51, "keys": 819, "parallelism": "single GPU"},
+                   "global_batch": 1, "seq_len": 51, "keys": 819, "parallelism": "single GPU",
+                   # the engine default; the reference re-rounds a bf16 diffusion_noise every
+                   # step (pipeline.py:105,132), selectable with fp32_euler=False
+                   "euler_accumulator": "fp32"},
         "ms_per_decoder_step": round(ms / STEPS, 4),
+        "launches_per_chunk": launches,
+        "graph_nodes": nodes,
+        "boundary_us": round(b_us, 3),
+        "sync_floor_ms": round(launches * b_us / 1000.0, 4),
+        "sync_floor_frac_of_value": round(launches * b_us / 1000.0 / ms, 4),
         "hbm_gbs": round(gbs, 1),
         "loop_roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
         "bytes_per_chunk": CHUNK_BYTES,

@@ -7,7 +7,8 @@ Backend contract (`backends/__init__.py:10-14` of the reference):
 from __future__ import annotations
 
 from . import encoder_wrappers, fused_wrappers, vision_wrappers, wrappers
-from .wrappers import attention_prefetch_for, prepare_weights, repack_stale, use_pool
+from .wrappers import (attention_prefetch_for, check_pinned, pin_packed_weights, prepare_weights,
+                       repack_stale, use_pool)
 
 # vision + encoder + decoder call sites (wrappers.py:393-403 of the reference), plus
 # `vision_attention` / `encoder_attention`, the functions the reference pipeline
@@ -21,6 +22,7 @@ FUSED_WRAPPERS = dict(fused_wrappers.FUSED_WRAPPERS)
 # Engine-level option outside the op table: `attention_prefetch_for(op)` returns the form
 # of this backend's decoder_attention that also prefetches the layer's FFN weights.
 
-__all__ = ["ALL_WRAPPERS", "FUSED_WRAPPERS", "attention_prefetch_for", "prepare_weights", "repack_stale", "use_pool",
+__all__ = ["ALL_WRAPPERS", "FUSED_WRAPPERS", "attention_prefetch_for", "check_pinned",
+           "pin_packed_weights", "prepare_weights", "repack_stale", "use_pool",
            "wrappers",
            "fused_wrappers", "encoder_wrappers", "vision_wrappers"]

@@ -152,7 +152,7 @@ def packed_weight_ptr(w: torch.Tensor, layout: int = 16, pad: tuple | None = Non
             raise ValueError("a padded weight must be a whole layer of its stack")
         return byte_off // layer_bytes * pad[0] * pad[1] * w.element_size()
     ptr = w.data_ptr()
-    for e in _PACKED:
+    for e in list(_PACKED):     # a copy: a weakref callback may remove entries meanwhile
         if (e.K == K and e.N == N and e.layout == layout and e.pad == pad
                 and e.base <= ptr < e.base + e.nbytes):
             src = e.src
@@ -203,7 +203,34 @@ def clear_packed_cache() -> None:
 
 def packed_cache_bytes() -> int:
     """Device bytes held by live packed copies."""
-    return sum(e.packed.numel() * e.packed.element_size() for e in _PACKED if e.src is not None)
+    return sum(e.packed.numel() * e.packed.element_size() for e in list(_PACKED)
+               if e.src is not None)
+
+
+def pin_packed_weights(weights) -> list:
+    """Strong references to the packed copies of `weights` (an engine's tensors).
+
+    A captured graph reads packed copies at fixed addresses. The cache itself holds
+    each source weakly and drops the copy with it, so an engine keeps the list this
+    returns for as long as its graph lives: then a source that is replaced rather
+    than updated in place leaves the graph reading stale but valid memory, and
+    `check_pinned` reports it."""
+    spans = [(t.data_ptr(), t.data_ptr() + t.numel() * t.element_size()) for t in weights]
+    return [e for e in list(_PACKED)
+            if any(lo <= e.base < hi for lo, hi in spans)]
+
+
+def check_pinned(pinned: list, weights) -> None:
+    """Raise if a pinned copy's source is no longer one of `weights`' storages (the
+    engine's weight was replaced by another tensor instead of updated in place)."""
+    live = {t.untyped_storage().data_ptr() for t in weights}
+    for e in pinned:
+        src = e.src
+        if src is None or src.untyped_storage().data_ptr() not in live:
+            raise RuntimeError(
+                "an engine weight was replaced rather than updated in place; the captured "
+                "graph still reads the old packed copy. Update weights in place "
+                "(engine.weights[name].copy_(new)) or build a new engine")
 
 
 def repack_stale() -> int:
@@ -346,15 +373,18 @@ def decoder_attention(Q, K, V, scores, out, encoder_seq_len):
     return out
 
 
-def _consumer_slices(M: int, w) -> int:
-    """Slices of packed `w` such that slice s is what workgroup s of its residual GEMM reads
-    (and so lands on XCD s % 8): row-split -> one column tile per slice (the tile's
-    workgroups sit on XCD nt % 8); split-K -> the (N / 16) x splitk K-slices."""
+def _consumer_slices(M: int, ld: int, addr: int, w) -> int:
+    """Slices of packed `w` such that slice s is what workgroup s of its residual GEMM
+    reads (and so lands on XCD s % 8) when its input is [M, K] with row pitch `ld` at
+    `addr`: row-split -> one column tile per slice (the tile's workgroups sit on XCD
+    nt % 8); split-K -> the (N / 16) x splitk K-slices. The choice is `_residual`'s own
+    predicate on the same operand."""
     Kw, Nw = w.shape
-    return (Nw // 16) * (1 if RESIDUAL_MODE == "rows" else _splitk(M, Nw, Kw))
+    return (Nw // 16) * (1 if _rows_ok_for(M, ld, addr, Kw, Nw) else _splitk(M, Nw, Kw))
 
 
-def decoder_attention_prefetch(Q, K, V, scores, out, encoder_seq_len, gate_w, up_w, down_w):
+def decoder_attention_prefetch(Q, K, V, scores, out, encoder_seq_len, gate_w, up_w, down_w,
+                               down_x=None):
     """`decoder_attention` whose spare workgroups also pull this layer's gate / up and
     down weights into the L2 of the XCDs that will read them (pi0hip_attention_prefetch).
     (Prefetching the o-proj's weights here, or the down's from spare workgroups of the
@@ -365,7 +395,8 @@ def decoder_attention_prefetch(Q, K, V, scores, out, encoder_seq_len, gate_w, up
     that of decoder_attention. Used for one request whose GEMMs take the skinny kernels,
     where workgroup s of the gate / up launch reads packed tile s and the residual GEMMs'
     workgroups read the slices `_consumer_slices` describes; otherwise it is plain
-    decoder_attention."""
+    decoder_attention. `down_x` is the down projection's input (the GeGLU activations);
+    without it an [M, K] row-major operand at a 16-byte aligned address is assumed."""
     rows = Q.shape[0]
     M = rows // DECODER_HEADS
     if K.dim() == 3 or M > _TILE_M:
@@ -378,7 +409,9 @@ def decoder_attention_prefetch(Q, K, V, scores, out, encoder_seq_len, gate_w, up
     regions = []
     for w in (gate_w, up_w):
         regions += [packed_weight_ptr(w), w.numel() * 2, w.shape[1] // 16]
-    regions += [packed_weight_ptr(down_w), down_w.numel() * 2, _consumer_slices(M, down_w)]
+    ld, addr = (down_w.shape[0], 0) if down_x is None else (down_x.stride(0), down_x.data_ptr())
+    regions += [packed_weight_ptr(down_w), down_w.numel() * 2,
+                _consumer_slices(M, ld, addr, down_w)]
     regions += [None, 0, 0]
     lib = _abi.lib()
     nbytes = lib.pi0hip_attention_batched_workspace_bytes(rows, keys, 1)
@@ -394,10 +427,15 @@ def attention_prefetch_for(attention_op):
     return decoder_attention_prefetch if attention_op is decoder_attention else None
 
 
+def _rows_ok_for(M: int, ld: int, addr: int, K: int, N: int) -> bool:
+    """The row-split kernel's shape rules (pi0hip_linear_residual_rows) for an [M, K]
+    operand with row pitch `ld` elements at device address `addr`."""
+    return (RESIDUAL_MODE == "rows" and M <= _TILE_M and K in (512, 1024, 2048, 4096)
+            and N % 16 == 0 and ld % 8 == 0 and addr % 16 == 0)
+
+
 def _rows_ok(x, K: int, N: int) -> bool:
-    """The row-split kernel's shape rules (pi0hip_linear_residual_rows)."""
-    return (RESIDUAL_MODE == "rows" and x.shape[0] <= _TILE_M and K in (512, 1024, 2048, 4096)
-            and N % 16 == 0 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0)
+    return _rows_ok_for(x.shape[0], x.stride(0), x.data_ptr(), K, N)
 
 
 # Residual GEMMs at M <= 64: "rows" = one launch of 16-row workgroups over the whole K

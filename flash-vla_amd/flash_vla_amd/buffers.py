@@ -22,14 +22,23 @@ from .spec import (DECODER_FFN, DECODER_HEADS, DECODER_LAYERS, DECODER_WIDTH, EN
 
 
 def rope_table(seq_len: int, offset: int, head_dim: int, device) -> torch.Tensor:
-    """Interleaved (cos, sin) bf16 table for positions [offset, offset + seq_len) (buffers.py:15-23)."""
-    positions = torch.arange(seq_len, device=device) + offset
-    inv_freq = 1.0 / (ROPE_THETA ** (torch.arange(0, head_dim, 2, dtype=torch.float32,
-                                                  device=device) / head_dim))
-    phase = inv_freq[None, :] * positions[:, None]
-    cos = torch.cos(phase).to(torch.bfloat16)
-    sin = torch.sin(phase).to(torch.bfloat16)
-    return torch.cat([cos[:, :, None], sin[:, :, None]], 2).view(-1, head_dim)
+    """RoPE operand of the QKV kernels: bf16 [seq_len, head_dim] (reference `buffers.py:15-23`).
+
+    Row r is position p = offset + r. Column pair (2j, 2j + 1) holds
+    (cos(p * w_j), sin(p * w_j)) with w_j = 1 / theta^(2j / head_dim), the
+    adjacent-pair rotation the packed Q/K columns use. Angles and their
+    cosines / sines are evaluated on the host in fp32 and rounded to bf16
+    once, so the table is the same bits whatever device it is copied to.
+    """
+    half = head_dim // 2
+    exponents = torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim
+    w = torch.pow(ROPE_THETA, exponents).reciprocal()
+    p = torch.arange(offset, offset + seq_len, dtype=torch.float32)
+    angles = torch.outer(p, w)                                    # [seq_len, half]
+    table = torch.empty(seq_len, half, 2, dtype=torch.bfloat16)
+    table[..., 0] = angles.cos()
+    table[..., 1] = angles.sin()
+    return table.reshape(seq_len, head_dim).to(device)
 
 
 def allocate_decoder_buffers(encoder_seq_len: int, chunk_size: int, device,

@@ -31,13 +31,60 @@ def _attention_prefetch(backend, ops, enabled: bool):
     return pick(ops.decoder_attention) if enabled and pick is not None else None
 
 
-def _refresh(backend) -> int:
+def _refresh(backend, pinned=None, weights=None) -> int:
     """Re-derive the backend's prepared (packed) weight copies from the engine's weights
     after they were updated in place; the captured graph reads the copies at fixed
     addresses, so its next replay uses the new values. Packed copies are not refreshed
-    during replay: weights are frozen between refreshes."""
+    during replay: weights are frozen between refreshes. A weight replaced by another
+    tensor (not updated in place) is an error: the graph cannot see it."""
+    check = getattr(backend, "check_pinned", None)
+    if check is not None and pinned:
+        check(pinned, weights)
     fn = getattr(backend, "repack_stale", None)
     return fn() if fn is not None else 0
+
+
+def _hip_runtime():
+    """The HIP runtime library this process already uses (the one torch loaded)."""
+    import ctypes
+    import re
+    with open("/proc/self/maps") as f:
+        paths = sorted(set(re.findall(r"(/\S*libamdhip64\.so\S*)", f.read())))
+    if not paths:
+        raise RuntimeError("the HIP runtime is not loaded")
+    return ctypes.CDLL(paths[0])
+
+
+_NODE_TYPES = {0: "kernel", 1: "memcpy", 2: "memset", 5: "empty"}
+
+
+def graph_node_counts(graph) -> dict:
+    """Nodes of a captured graph by type ({"kernel": n, "memcpy": n, ...}); `graph` must
+    have been created with keep_graph=True. Every kernel and copy node is one dependent
+    dispatch of the replay (the decoder graph is a single chain)."""
+    import ctypes
+    hip = _hip_runtime()
+    g = ctypes.c_void_p(graph.raw_cuda_graph())
+    n = ctypes.c_size_t(0)
+    if hip.hipGraphGetNodes(g, None, ctypes.byref(n)) != 0:
+        raise RuntimeError("hipGraphGetNodes failed")
+    nodes = (ctypes.c_void_p * n.value)()
+    if hip.hipGraphGetNodes(g, nodes, ctypes.byref(n)) != 0:
+        raise RuntimeError("hipGraphGetNodes failed")
+    counts: dict = {}
+    for node in nodes:
+        t = ctypes.c_int(-1)
+        if hip.hipGraphNodeGetType(ctypes.c_void_p(node), ctypes.byref(t)) != 0:
+            raise RuntimeError("hipGraphNodeGetType failed")
+        name = _NODE_TYPES.get(t.value, f"type{t.value}")
+        counts[name] = counts.get(name, 0) + 1
+    return counts
+
+
+def _pin(backend, weights) -> list:
+    """Keep the packed copies a captured graph reads alive as long as the engine."""
+    fn = getattr(backend, "pin_packed_weights", None)
+    return fn(list(weights.values())) if fn is not None else []
 
 
 class Pi0DecoderEngine:
@@ -46,13 +93,18 @@ class Pi0DecoderEngine:
     steps and layers exist for bisection, as in the reference engine. With `prefetch`
     (default) and a backend that offers it, each layer's attention launch also pulls the
     layer's FFN weights into L2 (same results; see `backends.hip.attention_prefetch_for`).
+    `batch` > 1 runs B independent requests through every GEMM at once (BASELINE config
+    5's decoder; not in the reference): each request has its own prefix K/V cache, and the
+    rows are stacked states first (the B state tokens, then the B x chunk action tokens).
     """
 
     def __init__(self, weights: dict, encoder_seq_len: int = 768, chunk_size: int = 50,
                  steps: int = 10, layers: int = 18, fused: bool = True, backend: str = "hip",
                  plan: dict | None = None, device: str = "cuda", capture: bool = True,
-                 warmup: int = 3, fp32_euler: bool = True, prefetch: bool = True):
+                 warmup: int = 3, fp32_euler: bool = True, prefetch: bool = True,
+                 batch: int = 1):
         self.encoder_seq_len = encoder_seq_len
+        self.batch = batch
         self.chunk_size = chunk_size
         self.steps = steps
         self.layers = layers
@@ -74,13 +126,14 @@ class Pi0DecoderEngine:
         self.buffers = allocate_decoder_buffers(
             encoder_seq_len, chunk_size, device, layers=n_layers, width=dims["width"],
             ffn=dims["ffn"], heads=dims["heads"], head_dim=dims["head_dim"],
-            action_dim=dims["action_dim"])
+            action_dim=dims["action_dim"], batch=batch)
         if fp32_euler:
             # the Euler accumulator stays fp32 between steps; diffusion_noise (bf16) is the output
             self.buffers["diffusion_noise_f32"] = torch.zeros(
-                chunk_size, dims["action_dim"], dtype=torch.float32, device=device)
+                batch * chunk_size, dims["action_dim"], dtype=torch.float32, device=device)
         self.pool = ScratchPool()
         self.graph = None
+        self._pinned = []
         if hasattr(self.backend, "prepare_weights"):
             self.backend.prepare_weights(self.weights)
         if capture:
@@ -104,26 +157,38 @@ class Pi0DecoderEngine:
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
         self.pool.freeze()
-        self.graph = torch.cuda.CUDAGraph()
+        self.graph = torch.cuda.CUDAGraph(keep_graph=True)
         with torch.cuda.graph(self.graph):
             self._run()
+        self.graph.instantiate()
+        self._pinned = _pin(self.backend, self.weights)
         torch.cuda.synchronize()
         self.buffers["diffusion_noise"].copy_(saved)
         self._sync_master()
+
+    def graph_nodes(self) -> dict:
+        """Nodes of the captured loop by type (see `graph_node_counts`)."""
+        return graph_node_counts(self.graph)
 
     def _sync_master(self):
         if "diffusion_noise_f32" in self.buffers:
             self.buffers["diffusion_noise_f32"].copy_(self.buffers["diffusion_noise"])
 
     def load_prefix(self, prefix_k: torch.Tensor, prefix_v: torch.Tensor) -> None:
-        """Copy the prefix K/V ([layers, >= enc_len, head_dim]) into the static cache."""
+        """Copy the prefix K/V ([layers, >= enc_len, head_dim]; batched: [B, layers, ...])
+        into the static cache."""
         e = self.encoder_seq_len
-        self.buffers["encoder_K"][:, :e].copy_(prefix_k[:, :e])
-        self.buffers["encoder_V"][:, :e].copy_(prefix_v[:, :e])
+        self.buffers["encoder_K"][..., :e, :].copy_(prefix_k[..., :e, :])
+        self.buffers["encoder_V"][..., :e, :].copy_(prefix_v[..., :e, :])
 
     def forward(self, state: torch.Tensor, noise: torch.Tensor) -> torch.Tensor:
-        """Denoise one action chunk; returns the static `diffusion_noise` buffer."""
-        self.buffers["observation_state_normalized"].copy_(state)
+        """Denoise one action chunk; returns the static `diffusion_noise` buffer.
+
+        Batched: state [B, 32] and noise [B, chunk, 32] or [B * chunk, 32]; the result
+        is [B * chunk, 32], request b in rows b * chunk .. (b + 1) * chunk - 1."""
+        self.buffers["observation_state_normalized"].copy_(
+            state.reshape(self.buffers["observation_state_normalized"].shape))
+        noise = noise.reshape(self.buffers["diffusion_noise"].shape)
         self.buffers["diffusion_noise"].copy_(noise)
         if "diffusion_noise_f32" in self.buffers:
             self.buffers["diffusion_noise_f32"].copy_(noise)
@@ -139,7 +204,7 @@ class Pi0DecoderEngine:
 
     def refresh_weights(self) -> int:
         """Call after updating `self.weights` in place (see `_refresh`)."""
-        return _refresh(self.backend)
+        return _refresh(self.backend, self._pinned, self.weights.values())
 
 
 class Pi0EncoderEngine:
@@ -173,6 +238,7 @@ class Pi0EncoderEngine:
             head_dim=head_dim, cache_len=cache_len)
         self.pool = ScratchPool()
         self.graph = None
+        self._pinned = []
         if hasattr(self.backend, "prepare_weights"):
             self.backend.prepare_weights(self.weights)
         if capture:
@@ -197,6 +263,7 @@ class Pi0EncoderEngine:
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             self._run()
+        self._pinned = _pin(self.backend, self.weights)
         torch.cuda.synchronize()
         self.buffers["encoder_x"].copy_(saved)
 
@@ -214,7 +281,7 @@ class Pi0EncoderEngine:
 
     def refresh_weights(self) -> int:
         """Call after updating `self.weights` in place (see `_refresh`)."""
-        return _refresh(self.backend)
+        return _refresh(self.backend, self._pinned, self.weights.values())
 
 
 class Pi0Inference:
@@ -278,6 +345,7 @@ class Pi0Inference:
                 device=device)
         self.pool = ScratchPool()
         self.graph = None
+        self._pinned = []
         if hasattr(self.backend, "prepare_weights"):
             self.backend.prepare_weights(self.weights)
         if capture:
@@ -318,6 +386,7 @@ class Pi0Inference:
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
             self._run()
+        self._pinned = _pin(self.backend, self.weights)
         torch.cuda.synchronize()
         self.buffers["diffusion_noise"].copy_(saved)
 
@@ -342,7 +411,7 @@ class Pi0Inference:
 
     def refresh_weights(self) -> int:
         """Call after updating `self.weights` in place (see `_refresh`)."""
-        return _refresh(self.backend)
+        return _refresh(self.backend, self._pinned, self.weights.values())
 
 
 def _dims_from(weights: dict) -> dict:

@@ -1,9 +1,12 @@
 """The encoder and decoder execution plans (mirror `hardware/nvidia/h100/pi0/pipeline.py:57-135`).
 
-Pure orchestration: every line is an op-table call on static buffers, so the
-loop captures into one hipGraph. Sequence = one state token + the action
-chunk; each Euler step re-projects the noise, runs the layers against the
-prefix KV cache and updates `diffusion_noise` in place.
+These functions allocate nothing and branch on nothing but shapes: each one
+issues a fixed sequence of op-table calls against buffers that already exist,
+which is what lets the engines record a whole forward as a single hipGraph.
+The decoder's token rows are the state token followed by the action chunk.
+Per Euler step the noise is projected back into the residual stream, the
+layers attend over the prefix K/V cache plus their own rows, and the
+out-projection adds the step's velocity into `diffusion_noise` in place.
 
 When the buffers also hold `diffusion_noise_f32`, that fp32 tensor is the Euler
 accumulator (read by the in-projection, updated by the out-projection) and is
@@ -138,7 +141,8 @@ def transformer_decoder(ops, weights, buffers, encoder_seq_len, steps=10, layers
                 ops.decoder_attention(*attn_args)
             else:   # same result; also pulls this layer's FFN weights into L2
                 attention_prefetch(*attn_args, weights["decoder_ffn_gate_w"][i],
-                                   weights["decoder_ffn_up_w"][i], weights["decoder_ffn_down_w"][i])
+                                   weights["decoder_ffn_up_w"][i], weights["decoder_ffn_down_w"][i],
+                                   down_x=buffers["decoder_hidden"])
             ops.decoder_out_proj_residual(
                 buffers["decoder_q_buf"].view(buffers["decoder_x"].shape[0], -1), weights["decoder_attn_o_w"][i],
                 buffers["decoder_x"])

@@ -136,8 +136,8 @@ int pi0hip_attention_batched(const void* q, int ldq, const void* k, const void* 
  * is skipped; pfr_bytes / pfr_slices must be a multiple of 128, pfr 4-byte aligned.
  * Loads only: `out` is bitwise that of pi0hip_attention. No reference counterpart
  * (the reference's decoder_attention, fused_wrappers.py:88-115, launches no prefetch);
- * the decoder engine passes the layer's o-proj, gate / up and down weights (their
- * launches read slice s on XCD s % 8). */
+ * the decoder engine passes the layer's gate, up and down weights in regions 0-2
+ * (their launches read slice s on XCD s % 8) and leaves region 3 null. */
 int pi0hip_attention_prefetch(const void* q, int ldq, const void* k, const void* v, int ldkv,
                               void* out, int ldo, int rows, int keys, int enc_len, int heads,
                               int head_dim, void* ws, size_t ws_bytes, const void* pf0,

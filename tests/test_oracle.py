@@ -88,6 +88,37 @@ def test_time_embedding_shape_and_endpoints():
     assert abs(emb[1, 3].item() - 1.0) < 1e-12
 
 
+def test_time_embedding_interior_known_answers():
+    """Hand-worked values at interior indices (Pi0: periods geometric from 4e-3 to 4).
+
+    Width 8 -> 4 periods 4e-3 * 1000^(i/3) = 0.004, 0.04, 0.4, 4. At t = 0.3 the
+    phases 2*pi*t/period are 150*pi, 15*pi, 1.5*pi and 0.15*pi, so
+    emb = [0, 0, -1, sin(0.15 pi) | 1, -1, 0, cos(0.15 pi)]. A linear period
+    spacing (0.004, 1.336, 2.668, 4) or swapped sin/cos halves fails at i = 1, 2.
+    Width 14 -> periods 4e-3 * 1000^(i/6): i = 2 is 0.04, i = 3 is 4e-3 * sqrt(1000).
+    """
+    from openpi_form import time_embedding
+
+    s15, c15 = math.sin(0.15 * math.pi), math.cos(0.15 * math.pi)
+    want8 = torch.tensor([0.0, 0.0, -1.0, s15, 1.0, -1.0, 0.0, c15], dtype=torch.float64)
+    got8 = W.sinusoidal_time_embedding(torch.tensor([0.3], dtype=torch.float64), 8)[0]
+    assert torch.allclose(got8, want8, atol=1e-9), got8
+    # t = 0.1: phases 50 pi, 5 pi, pi/2, 0.05 pi
+    want8b = torch.tensor([0.0, 0.0, 1.0, math.sin(0.05 * math.pi),
+                           1.0, -1.0, 0.0, math.cos(0.05 * math.pi)], dtype=torch.float64)
+    got8b = W.sinusoidal_time_embedding(torch.tensor([0.1], dtype=torch.float64), 8)[0]
+    assert torch.allclose(got8b, want8b, atol=1e-9), got8b
+    got14 = W.sinusoidal_time_embedding(torch.tensor([0.3], dtype=torch.float64), 14)[0]
+    assert abs(got14[2].item() - 0.0) < 1e-9 and abs(got14[7 + 2].item() + 1.0) < 1e-9
+    ph3 = 2 * math.pi * 0.3 / (4e-3 * math.sqrt(1000.0))
+    assert math.isclose(got14[3].item(), math.sin(ph3), abs_tol=1e-12)
+    assert math.isclose(got14[7 + 3].item(), math.cos(ph3), abs_tol=1e-12)
+    # the OpenPI-form test reference uses the same law
+    assert torch.allclose(time_embedding(0.3, 8), want8, atol=1e-9)
+    # and the packed schema's fp32 time grid reaches t = 0.3 at step 7 (fp32 accumulation)
+    assert abs(W.euler_times()[7].item() - 0.3) < 1e-6
+
+
 def test_rope_table_values():
     tab = O.rope_table(3, 768, 256, exact=True)
     # pair 0 has inv_freq 1: (cos 768, sin 768)
@@ -367,3 +398,11 @@ def test_unfused_rounding_points_known_answers():
     e = math.exp(1.0)
     assert p[0, 0].item() == O._bf(torch.tensor(e / (e + 1.0)), True).item()
     assert p[0, 1].item() == O._bf(torch.tensor(1.0 / (e + 1.0)), True).item()
+
+
+@pytest.mark.parametrize("offset", [0, 768, 816, 1024])
+def test_engine_rope_table_is_the_oracle_table_bitwise(offset):
+    """The engine's RoPE operand (built on the host) is the oracle's bf16 table bit for bit."""
+    from flash_vla_amd.buffers import rope_table
+    for rows in (51, 204):
+        assert torch.equal(rope_table(rows, offset, 256, "cpu"), O.rope_table(rows, offset, 256))
