@@ -302,3 +302,14 @@ def test_replaced_weight_is_reported_and_graph_memory_stays_valid(case):
     with pytest.raises(RuntimeError, match="replaced rather than updated in place"):
         eng.refresh_weights()
     del junk
+
+
+def test_graph_node_counts(case):
+    """The captured loop's dispatch count (the bench line's `launches_per_chunk`): per step
+    6 launches per layer (QKV, attention, merge, o-proj, gate, down) plus the action-in,
+    action-MLP (partials + reduce) and out-projection (partials + reduce) launches and the
+    state-row copy; once per chunk the state projection and the final fp32 -> bf16 copy."""
+    eng = _engine(case, 10, 18, capture=True)
+    nodes = eng.graph_nodes()
+    assert nodes.get("kernel") == 10 * (18 * 6 + 5) + 1 + 1, nodes
+    assert nodes.get("memcpy") == 10, nodes
