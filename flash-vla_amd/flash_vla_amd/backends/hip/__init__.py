@@ -6,7 +6,7 @@ Backend contract (`backends/__init__.py:10-14` of the reference):
 """
 from __future__ import annotations
 
-from . import encoder_wrappers, fused_wrappers, vision_wrappers, wrappers
+from . import encoder_wrappers, vision_wrappers, wrappers
 from .wrappers import (attention_prefetch_for, check_pinned, pin_packed_weights, prepare_weights,
                        repack_stale, use_pool)
 
@@ -18,11 +18,11 @@ ALL_WRAPPERS = {**vision_wrappers.VISION_WRAPPERS, **encoder_wrappers.ENCODER_WR
                 "vision_attention": vision_wrappers.vision_attention,
                 "encoder_attention": encoder_wrappers.encoder_attention,
                 "embed_prompt": encoder_wrappers.embed_prompt}
-FUSED_WRAPPERS = dict(fused_wrappers.FUSED_WRAPPERS)
+FUSED_WRAPPERS = dict(wrappers.FUSED_WRAPPERS)
 # Engine-level option outside the op table: `attention_prefetch_for(op)` returns the form
 # of this backend's decoder_attention that also prefetches the layer's FFN weights.
 
 __all__ = ["ALL_WRAPPERS", "FUSED_WRAPPERS", "attention_prefetch_for", "check_pinned",
            "pin_packed_weights", "prepare_weights", "repack_stale", "use_pool",
            "wrappers",
-           "fused_wrappers", "encoder_wrappers", "vision_wrappers"]
+           "encoder_wrappers", "vision_wrappers"]

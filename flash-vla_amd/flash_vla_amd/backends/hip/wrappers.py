@@ -612,3 +612,14 @@ ALL_WRAPPERS.update({
     "decoder_action_out_proj": decoder_action_out_proj_unfused,
     "decoder_attention": decoder_attention_unfused,
 })
+
+# op_table(fused=True) overlay, the names and semantics of the reference's fused overlay
+# (backends/tilelang/fused_wrappers.py:45-122): the gated FFN and the Euler out-projection
+# form their RMS factor inside the GEMM from its own A fragments and apply it to the fp32
+# accumulators (fused_norm.py:26-125); the attention keeps its score matrix inside the
+# kernel and ignores `scores` (base.py:801-923)
+FUSED_WRAPPERS = {
+    "decoder_norm_gated_ffn": decoder_norm_gated_ffn,
+    "decoder_action_out_proj": decoder_action_out_proj,
+    "decoder_attention": decoder_attention,
+}
