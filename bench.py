@@ -473,13 +473,19 @@ def main():
     print(f"[bench] {ms:.3f} ms/chunk (median of {args.steps}; bracket mean "
           f"{timing['ms_mean_bracket']:.3f})", file=sys.stderr, flush=True)
 
-    roof = None if args.no_kernel else kernel_roofline(eng, torch)
-    cpu = None if args.no_cpu else cpu_baseline()
     # lower-bound model of the loop: every kernel / copy node of the captured chain is one
     # dependent dispatch, and one dispatch costs at least an empty kernel's boundary
     nodes = eng.graph_nodes()
     launches = sum(v for k, v in nodes.items() if k in ("kernel", "memcpy", "memset"))
     b_us = boundary_us(torch)
+    roof = None if args.no_kernel else kernel_roofline(eng, torch)
+    if roof is not None:
+        # the same launches with the graph boundary (an empty kernel's cost, measured above)
+        # taken out: the kernel's own share of each launch (reported beside `frac`)
+        own = roof["avg_launch_us"] - b_us
+        roof["boundary_us"] = round(b_us, 3)
+        roof["frac_excl_boundary"] = round(GATE_BYTES / (own * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+    cpu = None if args.no_cpu else cpu_baseline()
 
     gbs = CHUNK_BYTES / (ms * 1e-3) / 1e9
     out = {
