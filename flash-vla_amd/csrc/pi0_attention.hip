@@ -417,14 +417,22 @@ int pi0hip_attention(const void* q, int ldq, const void* k, const void* v, int l
 // file-scope device array; every GPU the library runs on holds its own copy until the
 // process ends. Host code must not use the array's name as a device address: its address
 // on the current device comes from hipGetSymbolAddress, fetched once per device and cached.
+// The array holds NOALLOC_SLOTS slots of ATT_NOALLOC_SCRATCH_BYTES. A stream takes a slot
+// on its first call on a device and keeps it for the process, so calls on different
+// streams never share scratch; calls on one stream are ordered by the stream. A stream
+// beyond the slots is rejected (PI0HIP_ERR_WORKSPACE) rather than given a shared slot.
 constexpr size_t ATT_NOALLOC_SCRATCH_BYTES = size_t(8) << 20;
-static __device__ __align__(256) char scratch[ATT_NOALLOC_SCRATCH_BYTES];
+constexpr int NOALLOC_SLOTS = 4;
+static __device__ __align__(256) char scratch[NOALLOC_SLOTS * ATT_NOALLOC_SCRATCH_BYTES];
 
 static constexpr int MAX_DEVICES = 64;
 static std::mutex g_scratch_mu;
-static void* g_scratch_ptr[MAX_DEVICES];
+static char* g_scratch_ptr[MAX_DEVICES];
+static hipStream_t g_slot_stream[MAX_DEVICES][NOALLOC_SLOTS];
+static int g_slots_used[MAX_DEVICES];
 
-static int scratch_address(void** out) {
+// Scratch slot of stream `s` on the current device.
+static int scratch_slot(hipStream_t s, void** out) {
   int dev = 0;
   if (hipError_t e = hipGetDevice(&dev)) return (int)e;
   if (dev < 0 || dev >= MAX_DEVICES) return PI0HIP_ERR_ARG;
@@ -433,15 +441,24 @@ static int scratch_address(void** out) {
     void* p = nullptr;
     if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) return (int)e;
     if (!p) return PI0HIP_ERR_WORKSPACE;
-    g_scratch_ptr[dev] = p;
+    g_scratch_ptr[dev] = static_cast<char*>(p);
   }
-  *out = g_scratch_ptr[dev];
+  int slot = -1;
+  for (int i = 0; i < g_slots_used[dev]; ++i)
+    if (g_slot_stream[dev][i] == s) slot = i;
+  if (slot < 0) {
+    if (g_slots_used[dev] == NOALLOC_SLOTS) return PI0HIP_ERR_WORKSPACE;
+    slot = g_slots_used[dev]++;
+    g_slot_stream[dev][slot] = s;
+  }
+  *out = g_scratch_ptr[dev] + (size_t)slot * ATT_NOALLOC_SCRATCH_BYTES;
   return 0;
 }
 
 extern "C" {
 
 size_t pi0hip_attention_noalloc_max_bytes(void) { return ATT_NOALLOC_SCRATCH_BYTES; }
+int pi0hip_attention_noalloc_streams(void) { return NOALLOC_SLOTS; }
 
 int pi0hip_attention_noalloc(const void* q, int ldq, const void* k, const void* v, int ldkv,
                              void* out, int ldo, int rows, int keys, int enc_len, int heads,
@@ -450,9 +467,9 @@ int pi0hip_attention_noalloc(const void* q, int ldq, const void* k, const void* 
   const size_t need = pi0hip_attention_batched_workspace_bytes(rows, keys, 1);
   if (need > ATT_NOALLOC_SCRATCH_BYTES) return PI0HIP_ERR_WORKSPACE;
   void* ws = nullptr;
-  if (int e = scratch_address(&ws)) return e;
+  if (int e = scratch_slot(s, &ws)) return e;
   // every byte the kernels read from the workspace is written earlier in the same call, so
-  // nothing needs clearing; the contents left by the previous call are simply overwritten
+  // nothing needs clearing; the contents left by the stream's previous call are overwritten
   return attention_launch(q, ldq, k, v, ldkv, 0, out, ldo, rows, keys, enc_len, heads, head_dim,
                           1, ws, ATT_NOALLOC_SCRATCH_BYTES, 0, nullptr, nullptr, nullptr, s);
 }

@@ -37,6 +37,7 @@ PROTOTYPES = {
     "pi0hip_attention": (c_int, [P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int, c_int,
                                  c_int, P, c_size_t, P]),
     "pi0hip_attention_noalloc_max_bytes": (c_size_t, []),
+    "pi0hip_attention_noalloc_streams": (c_int, []),
     "pi0hip_attention_noalloc": (c_int, [P, c_int, P, P, c_int, P, c_int, c_int, c_int, c_int,
                                          c_int, c_int, P]),
     # unfused decoder call sites

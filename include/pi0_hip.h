@@ -207,13 +207,17 @@ int pi0hip_attention_unfused(const void* q, int ldq, const void* k, const void* 
                              hipStream_t s);
 
 /* pi0hip_attention without a workspace argument and without any allocation: the
- * partial outputs live in a static per-device array of pi0hip_attention_noalloc_max_bytes()
- * (8 MiB), enough for pi0hip_attention_workspace_bytes(rows, keys) up to e.g. 408 rows x
- * 2048 keys; larger shapes return PI0HIP_ERR_WORKSPACE without launching. Calls that
- * overlap on one GPU (several streams or threads at once) share the array and race.
+ * partial outputs live in a static per-device array of pi0hip_attention_noalloc_streams()
+ * (4) slots of pi0hip_attention_noalloc_max_bytes() (8 MiB) each, enough for
+ * pi0hip_attention_workspace_bytes(rows, keys) up to e.g. 408 rows x 2048 keys; larger
+ * shapes return PI0HIP_ERR_WORKSPACE without launching. Each stream takes its own slot on
+ * its first call on a device and keeps it until the process ends, so calls on different
+ * streams do not share scratch; a fifth stream on one device is rejected with
+ * PI0HIP_ERR_WORKSPACE. Calls on one stream run in stream order and reuse its slot.
  * No counterpart in the reference: for callers that cannot allocate device memory
  * (code under graph capture that may not call hipMalloc, tight serving loops). */
 size_t pi0hip_attention_noalloc_max_bytes(void);
+int pi0hip_attention_noalloc_streams(void);
 int pi0hip_attention_noalloc(const void* q, int ldq, const void* k, const void* v, int ldkv,
                              void* out, int ldo, int rows, int keys, int enc_len, int heads,
                              int head_dim, hipStream_t s);
