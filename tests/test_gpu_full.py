@@ -225,6 +225,33 @@ def test_full_forward_default_prompt_256():
     assert (1 - g_cos) <= 1.5 * (1 - e_cos) + 1e-6 and g_err <= 1.5 * e_err + 2e-3
 
 
+@pytest.mark.parametrize("views", [1, 4])
+def test_full_forward_other_view_counts(views):
+    """num_views other than 3 (the reference rejects only 2, pipeline.py:22): one view puts
+    256 rows through the vision and encoder GEMMs and 307 keys before the decoder rows;
+    four views 1024 rows and 1075 keys. 1 layer each, 1 Euler step, graph captured."""
+    from flash_vla_amd import Pi0Inference
+    ck = _shallow_checkpoint(seed=97 + views, vis=1, enc=1, dec=1)
+    g = torch.Generator().manual_seed(98 + views)
+    images = (torch.rand(views, 224, 224, 3, generator=g) * 2 - 1).to(torch.bfloat16)
+    state = torch.randn(32, generator=g).to(torch.bfloat16)
+    noise = torch.randn(50, 32, generator=g).to(torch.bfloat16)
+    print(f"full forward with {views} view(s)", flush=True)
+    eng = Pi0Inference({k: v.to(DEV) for k, v in ck.items()}, num_views=views, chunk_size=50,
+                       steps=1)
+    assert eng.encoder_seq_len == 256 * views
+    assert eng.buffers["encoder_K"].shape[1] == 256 * views + 51
+    out = eng.forward(images.to(DEV), state.to(DEV), noise.to(DEV)).clone()
+    bn, _, _ = Vn.full_forward(ck, images, state, noise, num_views=views, steps=1, bf16=True)
+    fn, _, _ = Vn.full_forward(ck, images, state, noise, num_views=views, steps=1, bf16=False)
+    g_err, g_cos = metrics(out, fn)
+    e_err, e_cos = metrics(bn, fn)
+    print(f"{views} view(s): gpu vs fp32 err {g_err:.3e} 1-cos {1 - g_cos:.2e}; "
+          f"bf16 oracle err {e_err:.3e} 1-cos {1 - e_cos:.2e}", flush=True)
+    assert g_cos >= 0.999
+    assert (1 - g_cos) <= 1.5 * (1 - e_cos) + 1e-6 and g_err <= 1.5 * e_err + 2e-3
+
+
 def test_full_forward_graph_equals_eager(full_case):
     from flash_vla_amd import Pi0Inference
     ck, images, state, noise = full_case
